@@ -1,0 +1,207 @@
+/* C ABI of librecap_hip.so: MI355X (gfx950) kernels of RECAP's corrected sparse-attention
+ * operator.  Paths in the citations are relative to the lyraxtg/RECAP tree.
+ *
+ * Conventions
+ *  - Every function returns 0 on success or a RECAP_E* code; recap_last_error() gives a
+ *    thread-local message for the last failure.  Arguments are validated on the host
+ *    before any launch; nothing is allocated and nothing synchronises the host.
+ *  - Device pointers are raw; the caller owns every buffer.  `stream` is a hipStream_t
+ *    (NULL = default stream); all work is enqueued on it.
+ *  - A "bank" is one (batch, head) pair, bank = b * heads + h.  Q/K/V are native-order
+ *    [batch, heads, tokens, dim] with element strides (stride_b, stride_h, stride_n) and a
+ *    unit stride on dim; rows and strides must keep 16-byte alignment.
+ *  - `rowmap[r]` (int32, [n_tokens]) is the native token of reordered row r: the Hilbert-
+ *    ordered video tokens first, then the text tokens (recap/sparse/layout.py:44-61).
+ *  - Block size is 128; dim is 64 or 128; dtype is RECAP_BF16 or RECAP_F16.
+ *  - Derived sizes: nb = ceil(n_video/128) video blocks, tb = ceil(n_tokens/128) kernel
+ *    blocks, R = floor(n_video/128)*128 refined rows.
+ */
+#ifndef RECAP_HIP_H
+#define RECAP_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RECAP_ABI_VERSION 1
+
+enum { RECAP_OK = 0, RECAP_EINVAL = 1, RECAP_EUNSUPPORTED = 2, RECAP_EHIP = 3 };
+enum { RECAP_F16 = 1, RECAP_BF16 = 2 };
+enum { RECAP_CLOSURE_ROT = 1, RECAP_CLOSURE_CVK = 2, RECAP_CLOSURE_SCATTER = 4 };
+
+int recap_abi_version(void);
+const char* recap_last_error(void);
+
+/* Hilbert order of a (frames, height, width) video grid, host only: out[i] is the native
+ * index t*H*W + y*W + x of reordered position i.
+ * Replaces hilbert_permutation, recap/sparse/geometry.py:27-67. */
+int recap_hilbert_permutation(int64_t frames, int64_t height, int64_t width, int64_t* out);
+
+/* Stage 1 ------------------------------------------------------------------------------ */
+
+/* fp32 means [banks, nb, dim] of the video tokens of x, gathered through rowmap.
+ * Replaces pool_blocks, recap/sparse/pooling.py:10-34 (query pooling of
+ * recap/sparse/attention.py:81). */
+int recap_pool_blocks(const void* x, int dtype, int64_t batch, int64_t heads, int64_t dim,
+                      int64_t stride_b, int64_t stride_h, int64_t stride_n,
+                      const int32_t* rowmap, int64_t n_tokens, int64_t n_video,
+                      float* means, void* stream);
+
+/* One pass over K and V: packed K tiles and V^T tiles [banks, tb, 128*dim] for the
+ * attention kernel, and the fp32 block means of K and V [banks, nb, dim].
+ * Replaces Layout.reorder of K/V (recap/operator.py:497-498), the permute copies of
+ * recap/kernels/block_sparse.py:112-114 and pool_blocks(K), pool_blocks(V)
+ * (recap/sparse/attention.py:173-174). */
+int recap_kv_pack(const void* k, const void* v, int dtype, int64_t batch, int64_t heads,
+                  int64_t dim, int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_n,
+                  int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_n,
+                  const int32_t* rowmap, int64_t n_tokens, int64_t n_video, void* k_tiles,
+                  void* vt_tiles, float* k_means, float* v_means, void* stream);
+
+/* fp32 block scores [banks, nb, nb] = fp32(scale) * (qbar . kbar), fixed summation order.
+ * Replaces the matmul + mul_ of block_proxy_mask, recap/sparse/router.py:18-19. */
+int recap_block_scores(const float* q_means, const float* k_means, int64_t banks,
+                       int64_t n_blocks, int64_t dim, float scale, float* scores, void* stream);
+
+/* Boolean partition [banks, nb, nb] (uint8 0/1): top-`keep` per row, ties to the lower
+ * index; force_last also selects the trailing partial block as row and column.
+ * Replaces topk + scatter of recap/sparse/router.py:20-22 and _match_kernel_granularity,
+ * recap/sparse/attention.py:84-94. */
+int recap_topk_blocks(const float* scores, int64_t banks, int64_t n_blocks, int64_t keep,
+                      int force_last, uint8_t* partition, void* stream);
+
+/* Kernel-grid mask [banks, tb, tb] with text/partial rows and columns dense.
+ * Replaces build_kernel_block_mask, recap/kernels/block_sparse.py:52-75. */
+int recap_kernel_block_mask(const uint8_t* partition, int64_t banks, int64_t n_tokens,
+                            int64_t n_video, uint8_t* kernel_mask, void* stream);
+
+/* work[0] = |new & old|, work[1] = |new| over `count` bytes; work holds 514 uint64.
+ * Replaces the overlap sums of recap/operator.py:423-428 (the caller reads the two counts
+ * to decide the rerank, as the reference does). */
+int recap_mask_overlap(const uint8_t* new_mask, const uint8_t* old_mask, int64_t count,
+                       uint64_t* work, void* stream);
+
+/* Stage 3 ------------------------------------------------------------------------------ */
+
+/* Number of partial groups of recap_closure_stats for `group` blocks per workgroup. */
+int64_t recap_closure_groups(int64_t n_video, int64_t group);
+
+/* Closure statistics from the packed tiles.  flags: ROT (needs u_hi_t/u_lo_t, writes
+ * variance [banks, nb, dim]), CVK (writes cvk_partial [banks, groups, dim, dim]),
+ * SCATTER (writes scatter_partial); allowed sets: ROT, CVK|SCATTER, ROT|CVK.
+ * Replaces rotated_leaf_moments_triton and pooled_cross_centered_triton_fp32,
+ * recap/kernels/closure_stats.py:96-290, and pooled_within_block_scatter,
+ * recap/sparse/closure.py:42-72. */
+int recap_closure_stats(const void* k_tiles, const void* vt_tiles, const float* k_means,
+                        int dtype, const void* u_hi_t, const void* u_lo_t, int64_t banks,
+                        int64_t dim, int64_t n_tokens, int64_t n_video, int64_t group,
+                        int flags, float* variance, float* cvk_partial, float* scatter_partial,
+                        void* stream);
+
+/* out[b, e] = sum_g partial[b, g, e] / divisor, fixed order over g.
+ * Replaces the final divisions of recap/kernels/closure_stats.py:290 and
+ * recap/sparse/closure.py:72. */
+int recap_partial_reduce(const float* partial, int64_t banks, int64_t groups, int64_t elems,
+                         float divisor, float* out, void* stream);
+
+/* Query-type tables of the coarse tail, [banks, nb, dim] each: w = fold_rank(variance,
+ * rank) with columns stored in swap23 order, kbar, vbar.
+ * Replaces fold_rank (recap/sparse/closure.py:96-104) and the casts of
+ * recap/kernels/coarse_tail.py:238-241. */
+int recap_coarse_tables(const float* variance, const float* k_means, const float* v_means,
+                        int dtype, int64_t banks, int64_t n_blocks, int64_t dim, int64_t rank,
+                        void* w, void* kbar, void* vbar, void* stream);
+
+/* Basis tables [banks, dim, dim]: U^T split hi/lo (closure statistics), U^T and C_vk in
+ * the query type (coarse tail).  Any output may be NULL; cvk may be NULL if cvk_t is.
+ * Replaces basis.to(dtype) / operator.to(dtype) of recap/sparse/closure.py:84-93 and the
+ * basis split of recap/kernels/closure_stats.py:133-135. */
+int recap_basis_tables(const float* basis, const float* cvk, int dtype, int64_t banks,
+                       int64_t dim, void* u_hi_t, void* u_lo_t, void* u_t, void* cvk_t,
+                       void* stream);
+
+/* Corrected coarse tail for the R refined rows: go [banks, R, dim] (query type),
+ * gl [banks, R] fp32; with glref [banks, R] also drift_partial [banks, R/128].
+ * Replaces coarse_tail_attention + _coarse_tail_kernel (recap/kernels/coarse_tail.py:
+ * 35-312), build_coarse_tail_plan (recap/sparse/planner.py:11-38), rotated_query_square
+ * and value_drift (recap/sparse/closure.py:84-93) and coarse_tail_apply
+ * (recap/sparse/attention.py:204-231). */
+int recap_coarse_tail(const void* q, int dtype, int64_t batch, int64_t heads, int64_t dim,
+                      int64_t stride_b, int64_t stride_h, int64_t stride_n,
+                      const int32_t* rowmap, const uint8_t* partition, const void* kbar,
+                      const void* vbar, const void* w, const void* u_t, const void* cvk_t,
+                      int64_t n_tokens, int64_t n_video, float scale, float theta,
+                      const float* glref, void* go, float* gl, float* drift_partial,
+                      void* stream);
+
+/* center[b] = sum(drift_partial[b, :]) / R.
+ * Replaces _drift_center, recap/operator.py:148-150. */
+int recap_drift_center(const float* drift_partial, int64_t banks, int64_t n_video,
+                       float* center, void* stream);
+
+/* Stage 2 ------------------------------------------------------------------------------ */
+
+/* Head branch at a refresh: exact attention over the kernel mask, reordered order:
+ * head_out [banks, n_tokens, dim] (query type), head_lse [banks, n_tokens] (natural log).
+ * Replaces block_sparse_exact, recap/kernels/block_sparse.py:78-139. */
+int recap_block_sparse_attn(const void* q, int dtype, int64_t batch, int64_t heads,
+                            int64_t dim, int64_t stride_b, int64_t stride_h, int64_t stride_n,
+                            const void* k_tiles, const void* vt_tiles, const int32_t* rowmap,
+                            const uint8_t* kernel_mask, int64_t n_tokens, float scale,
+                            void* head_out, float* head_lse, void* stream);
+
+/* Dense attention with LSE, native order: out [batch, heads, n_tokens, dim] with the
+ * given strides, lse [banks, n_tokens].
+ * Replaces aten._scaled_dot_product_flash_attention at recap/operator.py:254-256. */
+int recap_dense_attn(const void* q, int dtype, int64_t batch, int64_t heads, int64_t dim,
+                     int64_t stride_b, int64_t stride_h, int64_t stride_n, const void* k_tiles,
+                     const void* vt_tiles, const int32_t* rowmap, int64_t n_tokens, float scale,
+                     void* out, int64_t out_stride_b, int64_t out_stride_h,
+                     int64_t out_stride_n, float* lse, void* stream);
+
+/* The corrected sparse output in one pass: head attention with the merge of the coarse
+ * tail (go, gl), the refinement (det fp16 [banks, R, dim], dl [banks, R]) and the drift
+ * weight exp(-|gl - glref - center|) fused into the epilogue, stored in native order.
+ * alpha_override >= 0 replaces the drift weight (test knob; pass a negative value for
+ * the reference behaviour).
+ * Replaces block_sparse_exact + sparse_merge + Layout.restore, recap/operator.py:500-527
+ * and recap/kernels/detail_cache.py:188-301, 402-456. */
+int recap_sparse_merge_attn(const void* q, int dtype, int64_t batch, int64_t heads,
+                            int64_t dim, int64_t stride_b, int64_t stride_h, int64_t stride_n,
+                            const void* k_tiles, const void* vt_tiles, const int32_t* rowmap,
+                            const uint8_t* kernel_mask, int64_t n_tokens, int64_t n_video,
+                            float scale, const void* go, const float* gl, const void* det,
+                            const float* dl, const float* glref, const float* center,
+                            float alpha_override, void* out, int64_t out_stride_b,
+                            int64_t out_stride_h, int64_t out_stride_n, void* stream);
+
+/* Stage 4 ------------------------------------------------------------------------------ */
+
+/* Number of (err2, ref2) partial pairs recap_refresh_capture writes. */
+int64_t recap_capture_partials(int64_t banks, int64_t dim, int64_t n_video);
+
+/* Refinement capture in place into det (fp16 [banks, R, dim]) and dl ([banks, R]).  With
+ * glref and center non-NULL the previous refinement is scored first: stat_partial
+ * receives the partial pairs and stats[2] = (sum err^2, sum ref^2).
+ * Replaces refresh_detail + _refresh_detail_kernel, recap/kernels/detail_cache.py:25-186,
+ * 304-379. */
+int recap_refresh_capture(const void* dense_out, int dtype, int64_t batch, int64_t heads,
+                          int64_t dim, int64_t out_stride_b, int64_t out_stride_h,
+                          int64_t out_stride_n, const float* dense_lse, const void* head_out,
+                          const float* head_lse, const void* go, const float* gl,
+                          const int32_t* rowmap, int64_t n_tokens, int64_t n_video, void* det,
+                          float* dl, const float* glref, const float* center,
+                          float* stat_partial, float* stats, void* stream);
+
+/* Asynchronous copy of a refinement bank between pinned host memory and the device on
+ * `stream` (hipMemcpyAsync, direction inferred).
+ * Replaces the non_blocking copy_ of recap/host_banks.py:99-103. */
+int recap_bank_copy_async(void* dst, const void* src, int64_t bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RECAP_HIP_H */

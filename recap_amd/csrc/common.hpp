@@ -1,0 +1,129 @@
+// Shared device helpers for the gfx950 (CDNA4) kernels of the corrected sparse-attention
+// path: element types, MFMA wrappers, 64-wide wave reductions and packed-tile layouts.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace recap {
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kBlock = 128;        // tokens per block (query and key)
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// ---------------------------------------------------------------------------------------
+// Element types: values are stored as raw 16-bit words; arithmetic is fp32.
+
+struct BF16 {
+  static constexpr int code = 2;
+  __device__ static inline float to_f(uint16_t h) { return __uint_as_float((unsigned)h << 16); }
+  __device__ static inline uint16_t from_f(float f) {
+    return __builtin_bit_cast(uint16_t, (__bf16)f);  // round to nearest even
+  }
+  __device__ static inline f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+
+struct F16 {
+  static constexpr int code = 1;
+  __device__ static inline float to_f(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+  }
+  __device__ static inline uint16_t from_f(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+  }
+  __device__ static inline f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+
+__device__ inline float bf16_to_f(uint16_t h) { return BF16::to_f(h); }
+__device__ inline uint16_t f_to_bf16(float f) { return BF16::from_f(f); }
+__device__ inline float f16_to_f(uint16_t h) { return F16::to_f(h); }
+__device__ inline uint16_t f_to_f16(float f) { return F16::from_f(f); }
+
+template <class T>
+__device__ inline unsigned pack2(float lo, float hi) {
+  return (unsigned)T::from_f(lo) | ((unsigned)T::from_f(hi) << 16);
+}
+
+// ---------------------------------------------------------------------------------------
+// 32x32 MFMA output layout (all v_mfma_f32_32x32x* ops): lane l, register r holds
+// D[row = 8*(r/4) + 4*(l/32) + r%4][col = l%32].  A operand: lane l holds 8 consecutive
+// k of row l%32, k-group l/32.  B operand: lane l holds 8 consecutive k of column l%32.
+__device__ inline int mfma_row(int r, int g) { return 8 * (r >> 2) + 4 * g + (r & 3); }
+
+// Swap bits 2 and 3 of a position: maps an MFMA k-slot (8*g + e within a 16-group) to
+// the output row (8*(e/4) + 4*g + e%4) that held it, so a 32x32 result can feed the
+// next MFMA as its B operand without a register shuffle.
+__host__ __device__ inline int swap23(int p) {
+  return (p & ~12) | ((p & 4) << 1) | ((p & 8) >> 1);
+}
+
+// ---------------------------------------------------------------------------------------
+// Lane pairs (l, l^32) hold the two halves of one 32x32 output column.
+
+__device__ inline float pair_max(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ inline float pair_sum(float x) {
+  // Both lanes compute low-half + high-half in the same order.
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Fixed-order sum over lanes 0..31 of a wave (butterfly), result in every lane.
+__device__ inline float half_wave_sum(float x) {
+  for (int off = 16; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+
+__device__ inline float wave_sum(float x) {
+  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+
+// ---------------------------------------------------------------------------------------
+// Work-item order: blockIdx -> linear item so that each XCD (8 per MI355X, workgroups
+// dealt round-robin) gets a contiguous range of items and hence of banks, keeping one
+// bank's K/V tiles in that XCD's L2.
+__device__ inline int xcd_linear(int bid, int n) {
+  const int xcd = bid & 7, slot = bid >> 3;
+  const int per = n >> 3, rem = n & 7;
+  return xcd * per + min(xcd, rem) + slot;
+}
+
+// Packed tile geometry: a K tile is [128 keys][D] with its 16-byte chunks XOR-swizzled
+// by key row; a V^T tile is [D][128 positions] where position p holds key swap23(p),
+// chunks swizzled by the d row.  The images are copied verbatim into LDS.
+template <int D>
+struct TileGeom {
+  static constexpr int kRowBytes = D * 2;           // K tile row
+  static constexpr int kChunks = D / 8;             // 16-byte chunks per K row
+  static constexpr int kTileElems = kBlock * D;     // elements per K (or V^T) tile
+  static constexpr int kTileBytes = kTileElems * 2;
+  __host__ __device__ static inline int k_off(int key, int chunk) {  // bytes
+    return key * kRowBytes + ((chunk ^ (key & (kChunks - 1))) << 4);
+  }
+  __host__ __device__ static inline int vt_off(int d, int chunk) {  // bytes, 16 chunks/row
+    return d * 256 + ((chunk ^ (d & 15)) << 4);
+  }
+};
+
+__device__ inline u32x4 lds_load16(const char* base, int off) {
+  return *reinterpret_cast<const u32x4*>(base + off);
+}
+
+}  // namespace recap

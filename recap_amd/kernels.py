@@ -1,0 +1,359 @@
+"""torch-facing wrappers of the HIP kernels: argument checks, output allocation, streams.
+
+Every function runs on ``torch.cuda.current_stream()`` and allocates its outputs with the
+caching allocator; the kernels themselves never allocate.  Tensors are passed to the C ABI
+as raw device pointers with explicit strides.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import call
+
+BLOCK = 128
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.bfloat16:
+        return _lib.RECAP_BF16
+    if dtype == torch.float16:
+        return _lib.RECAP_F16
+    raise ValueError(f"unsupported attention dtype {dtype}; use bfloat16 or float16")
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _p(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+@dataclass(frozen=True)
+class Geometry:
+    """Block geometry of one sequence (recap/sparse/attention.py:42-52,
+    recap/kernels/block_sparse.py:60-74)."""
+
+    n_tokens: int
+    n_video: int
+
+    @property
+    def nb(self) -> int:
+        return (self.n_video + BLOCK - 1) // BLOCK
+
+    @property
+    def tb(self) -> int:
+        return (self.n_tokens + BLOCK - 1) // BLOCK
+
+    @property
+    def ds(self) -> int:
+        shared = self.n_video % BLOCK != 0 and self.n_tokens > self.n_video
+        return self.nb - 1 if shared else self.nb
+
+    @property
+    def rows(self) -> int:
+        return (self.n_video // BLOCK) * BLOCK
+
+    @property
+    def partial(self) -> bool:
+        return self.n_video % BLOCK != 0
+
+    def counts(self, device) -> torch.Tensor:
+        c = torch.full((self.nb,), float(BLOCK), dtype=torch.float32, device=device)
+        c[-1] = float(self.n_video - BLOCK * (self.nb - 1))
+        return c
+
+
+def prepare(x: torch.Tensor, name: str) -> torch.Tensor:
+    """A ``[B, H, N, D]`` view the kernels can read: unit dim stride, strides and base
+    pointer 16-byte aligned; otherwise a contiguous copy."""
+    if x.ndim != 4:
+        raise ValueError(f"{name} must be [batch, heads, tokens, dim], got {tuple(x.shape)}")
+    if not x.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor")
+    dtype_code(x.dtype)
+    if x.shape[-1] not in (64, 128):
+        raise ValueError(f"{name}: head dim {x.shape[-1]} unsupported (64 or 128)")
+    ok = (x.stride(-1) == 1 and all(s % 8 == 0 for s in x.stride()[:3])
+          and x.data_ptr() % 16 == 0)
+    if not ok:
+        x = x.contiguous()
+        if x.data_ptr() % 16:
+            x = x.clone()
+    return x
+
+
+def _qkv_args(x: torch.Tensor):
+    b, h, _, d = x.shape
+    return [x.data_ptr(), dtype_code(x.dtype), b, h, d, x.stride(0), x.stride(1), x.stride(2)]
+
+
+# -- stage 1 -------------------------------------------------------------------------------
+
+
+@dataclass
+class PackedKV:
+    """Packed K / V^T tiles and fp32 block means of one call."""
+
+    k_tiles: torch.Tensor   # [banks, tb, 128*d] (K tile images)
+    vt_tiles: torch.Tensor  # [banks, tb, 128*d] (V^T tile images)
+    k_means: torch.Tensor   # [banks, nb, d] fp32
+    v_means: torch.Tensor   # [banks, nb, d] fp32
+    dtype: torch.dtype
+    dim: int
+
+
+def kv_pack(k: torch.Tensor, v: torch.Tensor, rowmap: torch.Tensor, geo: Geometry) -> PackedKV:
+    if k.shape != v.shape or k.dtype != v.dtype:
+        raise ValueError("K and V must have the same shape and dtype")
+    b, h, n, d = k.shape
+    banks = b * h
+    kt = torch.empty(banks, geo.tb, BLOCK * d, dtype=k.dtype, device=k.device)
+    vt = torch.empty_like(kt)
+    km = torch.empty(banks, geo.nb, d, dtype=torch.float32, device=k.device)
+    vm = torch.empty_like(km)
+    call("recap_kv_pack", k.data_ptr(), v.data_ptr(), dtype_code(k.dtype), b, h, d,
+         k.stride(0), k.stride(1), k.stride(2), v.stride(0), v.stride(1), v.stride(2),
+         rowmap.data_ptr(), n, geo.n_video, kt.data_ptr(), vt.data_ptr(), km.data_ptr(),
+         vm.data_ptr(), _stream())
+    return PackedKV(kt, vt, km, vm, k.dtype, d)
+
+
+def pool_blocks(x: torch.Tensor, rowmap: torch.Tensor, geo: Geometry) -> torch.Tensor:
+    b, h, n, d = x.shape
+    out = torch.empty(b * h, geo.nb, d, dtype=torch.float32, device=x.device)
+    call("recap_pool_blocks", *_qkv_args(x), rowmap.data_ptr(), n, geo.n_video, out.data_ptr(),
+         _stream())
+    return out
+
+
+def block_scores(q_means: torch.Tensor, k_means: torch.Tensor, scale: float) -> torch.Tensor:
+    banks, nb, d = q_means.shape
+    out = torch.empty(banks, nb, nb, dtype=torch.float32, device=q_means.device)
+    call("recap_block_scores", q_means.data_ptr(), k_means.data_ptr(), banks, nb, d,
+         float(scale), out.data_ptr(), _stream())
+    return out
+
+
+def topk_blocks(scores: torch.Tensor, keep: int, force_last: bool) -> torch.Tensor:
+    banks, nb, _ = scores.shape
+    out = torch.empty(banks, nb, nb, dtype=torch.bool, device=scores.device)
+    call("recap_topk_blocks", scores.data_ptr(), banks, nb, int(keep), int(bool(force_last)),
+         out.data_ptr(), _stream())
+    return out
+
+
+def kernel_block_mask(partition: torch.Tensor, geo: Geometry) -> torch.Tensor:
+    banks = partition.numel() // (geo.nb * geo.nb)
+    partition = partition.contiguous()
+    out = torch.empty(banks, geo.tb, geo.tb, dtype=torch.bool, device=partition.device)
+    call("recap_kernel_block_mask", partition.data_ptr(), banks, geo.n_tokens, geo.n_video,
+         out.data_ptr(), _stream())
+    return out
+
+
+def mask_overlap(new: torch.Tensor, old: torch.Tensor) -> tuple[int, int]:
+    """(|new & old|, |new|); synchronises the stream to read the counts, as the reference's
+    ``float(kept)`` does (recap/operator.py:427)."""
+    new, old = new.contiguous(), old.contiguous()
+    work = torch.empty(514, dtype=torch.int64, device=new.device)
+    call("recap_mask_overlap", new.data_ptr(), old.data_ptr(), new.numel(), work.data_ptr(),
+         _stream())
+    kept, total = work[:2].tolist()
+    return int(kept), int(total)
+
+
+def select_blocks(q: torch.Tensor, k_means: torch.Tensor, rowmap: torch.Tensor, geo: Geometry,
+                  density: float, scale: float) -> torch.Tensor:
+    """Partition ``[banks, nb, nb]`` bool (recap/sparse/attention.py:74-94)."""
+    q_means = pool_blocks(q, rowmap, geo)
+    keep = max(1, round(float(density) * geo.nb))
+    keep = min(keep, geo.nb)
+    return topk_blocks(block_scores(q_means, k_means, scale), keep, geo.partial)
+
+
+# -- stage 3 -------------------------------------------------------------------------------
+
+
+CLOSURE_GROUP = 8
+
+
+def closure_stats(kv: PackedKV, geo: Geometry, flags: int, u_hi_t=None, u_lo_t=None,
+                  group: int = CLOSURE_GROUP):
+    """(variance, C_vk, scatter) for the requested statistics; absent ones are None."""
+    banks, d = kv.k_means.shape[0], kv.dim
+    dev = kv.k_means.device
+    groups = int(_lib.load().recap_closure_groups(geo.n_video, group))
+    var = cvk_part = scat_part = None
+    if flags & _lib.CLOSURE_ROT:
+        var = torch.empty(banks, geo.nb, d, dtype=torch.float32, device=dev)
+    if flags & _lib.CLOSURE_CVK:
+        cvk_part = torch.empty(banks, groups, d, d, dtype=torch.float32, device=dev)
+    if flags & _lib.CLOSURE_SCATTER:
+        scat_part = torch.empty(banks, groups, d, d, dtype=torch.float32, device=dev)
+    call("recap_closure_stats", kv.k_tiles.data_ptr(), kv.vt_tiles.data_ptr(),
+         kv.k_means.data_ptr(), dtype_code(kv.dtype), _p(u_hi_t), _p(u_lo_t), banks, d,
+         geo.n_tokens, geo.n_video, group, flags, _p(var), _p(cvk_part), _p(scat_part), _stream())
+    cvk = scatter = None
+    if cvk_part is not None:
+        cvk = partial_reduce(cvk_part, float(geo.n_video))
+    if scat_part is not None:
+        scatter = partial_reduce(scat_part, float(geo.n_video))
+    return var, cvk, scatter
+
+
+def partial_reduce(part: torch.Tensor, divisor: float) -> torch.Tensor:
+    banks, groups = part.shape[:2]
+    elems = part[0, 0].numel()
+    out = torch.empty(banks, *part.shape[2:], dtype=torch.float32, device=part.device)
+    call("recap_partial_reduce", part.data_ptr(), banks, groups, elems, float(divisor),
+         out.data_ptr(), _stream())
+    return out
+
+
+@dataclass
+class BasisTables:
+    u_hi_t: torch.Tensor | None = None
+    u_lo_t: torch.Tensor | None = None
+    u_t: torch.Tensor | None = None
+    cvk_t: torch.Tensor | None = None
+
+
+def basis_tables(basis: torch.Tensor | None, cvk: torch.Tensor | None, dtype: torch.dtype, *,
+                 split: bool = False, query: bool = False, cvk_table: bool = False) -> BasisTables:
+    src = basis if basis is not None else cvk
+    banks, d = src.shape[0], src.shape[-1]
+    mk = lambda: torch.empty(banks, d, d, dtype=dtype, device=src.device)  # noqa: E731
+    out = BasisTables(u_hi_t=mk() if split else None, u_lo_t=mk() if split else None,
+                      u_t=mk() if query else None, cvk_t=mk() if cvk_table else None)
+    dummy = basis if basis is not None else cvk
+    call("recap_basis_tables", dummy.data_ptr(), _p(cvk), dtype_code(dtype), banks, d,
+         _p(out.u_hi_t), _p(out.u_lo_t), _p(out.u_t), _p(out.cvk_t), _stream())
+    return out
+
+
+def coarse_tables(var: torch.Tensor, kv: PackedKV, rank: int):
+    banks, nb, d = var.shape
+    mk = lambda: torch.empty(banks, nb, d, dtype=kv.dtype, device=var.device)  # noqa: E731
+    w, kbar, vbar = mk(), mk(), mk()
+    call("recap_coarse_tables", var.data_ptr(), kv.k_means.data_ptr(), kv.v_means.data_ptr(),
+         dtype_code(kv.dtype), banks, nb, d, int(rank), w.data_ptr(), kbar.data_ptr(),
+         vbar.data_ptr(), _stream())
+    return w, kbar, vbar
+
+
+def coarse_tail(q: torch.Tensor, rowmap: torch.Tensor, partition: torch.Tensor, geo: Geometry,
+                tables: dict, scale: float, theta: float, glref: torch.Tensor | None = None):
+    """(go [banks, R, d], gl [banks, R], drift partial [banks, R/128] or None)."""
+    b, h, n, d = q.shape
+    banks = b * h
+    go = torch.empty(banks, geo.rows, d, dtype=q.dtype, device=q.device)
+    gl = torch.empty(banks, geo.rows, dtype=torch.float32, device=q.device)
+    part = None
+    if glref is not None:
+        part = torch.empty(banks, max(1, geo.rows // BLOCK), dtype=torch.float32, device=q.device)
+    call("recap_coarse_tail", *_qkv_args(q), rowmap.data_ptr(), partition.data_ptr(),
+         tables["kbar"].data_ptr(), tables["vbar"].data_ptr(), tables["w"].data_ptr(),
+         tables["u_t"].data_ptr(), tables["cvk_t"].data_ptr(), n, geo.n_video, float(scale),
+         float(theta), _p(glref), go.data_ptr(), gl.data_ptr(), _p(part), _stream())
+    return go, gl, part
+
+
+def drift_center(part: torch.Tensor, geo: Geometry) -> torch.Tensor:
+    banks = part.shape[0]
+    out = torch.empty(banks, dtype=torch.float32, device=part.device)
+    call("recap_drift_center", part.data_ptr(), banks, geo.n_video, out.data_ptr(), _stream())
+    return out
+
+
+# -- stage 2 -------------------------------------------------------------------------------
+
+
+def block_sparse_attn(q: torch.Tensor, kv: PackedKV, rowmap: torch.Tensor,
+                      kernel_mask: torch.Tensor, geo: Geometry, scale: float):
+    """Head branch (reordered order): (out [banks, N, d], lse [banks, N])."""
+    b, h, n, d = q.shape
+    out = torch.empty(b * h, n, d, dtype=q.dtype, device=q.device)
+    lse = torch.empty(b * h, n, dtype=torch.float32, device=q.device)
+    call("recap_block_sparse_attn", *_qkv_args(q), kv.k_tiles.data_ptr(), kv.vt_tiles.data_ptr(),
+         rowmap.data_ptr(), kernel_mask.data_ptr(), n, float(scale), out.data_ptr(),
+         lse.data_ptr(), _stream())
+    return out, lse
+
+
+def dense_attn(q: torch.Tensor, kv: PackedKV, rowmap: torch.Tensor, scale: float,
+               out: torch.Tensor | None = None):
+    """Dense attention, native order: (out [B, H, N, d], lse [B, H, N])."""
+    b, h, n, d = q.shape
+    if out is None:
+        out = torch.empty(b, h, n, d, dtype=q.dtype, device=q.device)
+    lse = torch.empty(b, h, n, dtype=torch.float32, device=q.device)
+    call("recap_dense_attn", *_qkv_args(q), kv.k_tiles.data_ptr(), kv.vt_tiles.data_ptr(),
+         rowmap.data_ptr(), n, float(scale), out.data_ptr(), out.stride(0), out.stride(1),
+         out.stride(2), lse.data_ptr(), _stream())
+    return out, lse
+
+
+def sparse_merge_attn(q: torch.Tensor, kv: PackedKV, rowmap: torch.Tensor,
+                      kernel_mask: torch.Tensor, geo: Geometry, scale: float, go, gl, det, dl,
+                      glref, center, alpha_override: float | None = None,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+    """Corrected sparse output [B, H, N, d] in native order (one fused kernel)."""
+    b, h, n, d = q.shape
+    if out is None:
+        out = torch.empty(b, h, n, d, dtype=q.dtype, device=q.device)
+    alpha = -1.0 if alpha_override is None else float(alpha_override)
+    call("recap_sparse_merge_attn", *_qkv_args(q), kv.k_tiles.data_ptr(),
+         kv.vt_tiles.data_ptr(), rowmap.data_ptr(), kernel_mask.data_ptr(), n, geo.n_video,
+         float(scale), _p(go), _p(gl), _p(det), _p(dl), _p(glref), _p(center), alpha,
+         out.data_ptr(), out.stride(0), out.stride(1), out.stride(2), _stream())
+    return out
+
+
+# -- stage 4 -------------------------------------------------------------------------------
+
+
+def refresh_capture(dense_out: torch.Tensor, dense_lse: torch.Tensor, head_out: torch.Tensor,
+                    head_lse: torch.Tensor, go: torch.Tensor, gl: torch.Tensor,
+                    rowmap: torch.Tensor, geo: Geometry, det: torch.Tensor, dl: torch.Tensor,
+                    glref: torch.Tensor | None = None, center: torch.Tensor | None = None):
+    """Write the refinement in place; with (glref, center) return the validation pair."""
+    b, h, n, d = dense_out.shape
+    stats = part = None
+    if glref is not None:
+        npart = int(_lib.load().recap_capture_partials(b * h, d, geo.n_video))
+        part = torch.empty(max(1, npart), 2, dtype=torch.float32, device=dense_out.device)
+        stats = torch.empty(2, dtype=torch.float32, device=dense_out.device)
+    call("recap_refresh_capture", dense_out.data_ptr(), dtype_code(dense_out.dtype), b, h, d,
+         dense_out.stride(0), dense_out.stride(1), dense_out.stride(2), dense_lse.data_ptr(),
+         head_out.data_ptr(), head_lse.data_ptr(), go.data_ptr(), gl.data_ptr(),
+         rowmap.data_ptr(), n, geo.n_video, det.data_ptr(), dl.data_ptr(), _p(glref),
+         _p(center), _p(part), _p(stats), _stream())
+    return stats
+
+
+def bank_copy_async(dst: torch.Tensor, src: torch.Tensor, stream=None) -> None:
+    """Asynchronous device <-> pinned-host copy of a whole bank tensor on ``stream``."""
+    if dst.numel() * dst.element_size() != src.numel() * src.element_size():
+        raise ValueError("bank copy size mismatch")
+    if not (dst.is_contiguous() and src.is_contiguous()):
+        raise ValueError("bank copies need contiguous tensors")
+    handle = (stream or torch.cuda.current_stream()).cuda_stream
+    call("recap_bank_copy_async", dst.data_ptr(), src.data_ptr(),
+         dst.numel() * dst.element_size(), handle)
+
+
+def hilbert_permutation_native(grid) -> "torch.Tensor":
+    frames, height, width = (int(x) for x in grid)
+    out = torch.empty(frames * height * width, dtype=torch.int64)
+    call("recap_hilbert_permutation", frames, height, width, out.data_ptr())
+    return out
+
+
+def scale_for(dim: int) -> float:
+    return 1.0 / math.sqrt(dim)

@@ -1,0 +1,444 @@
+"""Attention for the EXACT, REFRESH and SPARSE steps on MI355X (recap/operator.py).
+
+``EXACT``    dense attention (torch SDPA, as the reference).
+``REFRESH``  dense attention with LSE on the HIP kernel; stores the refinement (exact tail
+             minus coarse tail) and measures the error of the previous one.
+``SPARSE``   the corrected sparse call: selected blocks exactly, the coarse tail over the
+             omitted blocks, and the cached refinement weighted by the drift weight,
+             merged in log-mass space -- four HIP stages:
+
+    kv_pack          K/V gathered through the Hilbert row map into packed tiles + block means
+    closure_stats    rotated block variances and C_vk (the frozen basis from the first call)
+    coarse_tail      corrected coarse attention over the omitted blocks + drift partials
+    sparse_merge_attn  block-sparse flash attention with the merge fused in its epilogue,
+                     stored straight to native order
+
+The public surface (``build``, ``reset``, ``begin_step``, ``set_stream``, ``attend``,
+``banks_valid``, ``n_streams``, ``drain_validation``, ``peak_bank_bytes``, ``layout``) is
+the reference's, so the diffusers processors call it unchanged.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+from . import kernels as K
+from .config import OperatorConfig
+from .layout import Layout, SparseGeometry
+
+EXACT = "exact"
+REFRESH = "refresh"
+SPARSE = "sparse"
+
+
+class SparseAttention:
+    """Per-layer state: the covariance basis frozen at the first call of a sample
+    (recap/sparse/attention.py:60-231), with its query-type tables cached."""
+
+    def __init__(self, geometry: SparseGeometry, config: OperatorConfig):
+        self.geometry = geometry
+        self.config = config
+        self.reset()
+
+    def reset(self) -> None:
+        self._basis: torch.Tensor | None = None
+        self._tables: K.BasisTables | None = None
+
+    @property
+    def basis(self) -> torch.Tensor | None:
+        return self._basis
+
+    def head_partition(self, q: torch.Tensor, kv: K.PackedKV, rowmap: torch.Tensor,
+                       geo: K.Geometry, scale: float) -> torch.Tensor:
+        """Selected key blocks ``[banks, nb, nb]`` (recap/sparse/attention.py:74-94)."""
+        return K.select_blocks(q, kv.k_means, rowmap, geo, self.config.head_density, scale)
+
+    def coarse_tail_context(self, kv: K.PackedKV, geo: K.Geometry) -> dict:
+        """Partition-independent statistics (recap/sparse/attention.py:98-202)."""
+        dtype = kv.dtype
+        if self._basis is None:
+            _, cvk, scatter = K.closure_stats(kv, geo, _lib.CLOSURE_CVK | _lib.CLOSURE_SCATTER)
+            symmetric = 0.5 * (scatter + scatter.transpose(-1, -2))
+            basis = torch.linalg.eigh(symmetric)[1].contiguous()
+            split = K.basis_tables(basis, None, dtype, split=True)
+            var, _, _ = K.closure_stats(kv, geo, _lib.CLOSURE_ROT, split.u_hi_t, split.u_lo_t)
+            # Order the basis by pooled within-block variance (recap/sparse/attention.py:137-152).
+            weights = geo.counts(var.device).reshape(1, -1, 1)
+            pooled = (var * weights).sum(1) / weights.sum().clamp_min(1.0)
+            order = torch.argsort(pooled, dim=-1, descending=True)
+            idx = order.unsqueeze(1)
+            basis = torch.gather(basis, 2, idx.expand(-1, basis.shape[1], -1)).contiguous()
+            var = torch.gather(var, 2, idx.expand(-1, var.shape[1], -1)).contiguous()
+            self._basis = basis
+            self._tables = K.basis_tables(basis, None, dtype, split=True, query=True)
+        else:
+            var, cvk, _ = K.closure_stats(kv, geo, _lib.CLOSURE_ROT | _lib.CLOSURE_CVK,
+                                          self._tables.u_hi_t, self._tables.u_lo_t)
+        cvk_t = K.basis_tables(None, cvk, dtype, cvk_table=True).cvk_t
+        w, kbar, vbar = K.coarse_tables(var, kv, int(self.config.closure_rank))
+        return {"w": w, "kbar": kbar, "vbar": vbar, "u_t": self._tables.u_t, "cvk_t": cvk_t,
+                "variance": var, "cvk": cvk}
+
+    def coarse_tail_apply(self, q, rowmap, context, partition, geo, scale, glref=None):
+        """Coarse tail over the omitted blocks (recap/sparse/attention.py:204-231)."""
+        return K.coarse_tail(q, rowmap, partition, geo, context, scale,
+                             self.config.closure_gate_theta, glref)
+
+
+@dataclass
+class DetailBank:
+    """One layer's cached refinement and its partition (recap/operator.py:33-59)."""
+
+    head_kernel_mask: torch.Tensor | None = None  # [banks, tb, tb] bool
+    partition: torch.Tensor | None = None         # [B, H, nb, nb] bool
+    value: torch.Tensor | None = None             # [banks, rows, dim] fp16
+    log_mass: torch.Tensor | None = None          # [banks, rows] fp32
+    coarse_lse: torch.Tensor | None = None        # [banks, rows] fp32
+    valid: bool = False
+    refreshed_at: int = 0
+    pending_stats: torch.Tensor | None = None     # [2] fp32
+    pending_age: int | None = None
+
+    def release(self) -> None:
+        self.head_kernel_mask = self.partition = None
+        self.value = self.log_mass = self.coarse_lse = None
+        self.valid = False
+        self.refreshed_at = 0
+        self.pending_stats = None
+        self.pending_age = None
+
+
+class BankChunk:
+    """A DetailBank restricted to a range of banks (``bank_chunks``, recap/operator.py:62-145).
+
+    Tensor fields read as views of the layer-wide tensors and write through into them;
+    the layer-level flags are published by ``commit`` after all groups have run.
+    """
+
+    _TENSORS = ("head_kernel_mask", "partition", "value", "log_mass", "coarse_lse")
+
+    def __init__(self, bank: DetailBank, *, lo: int, hi: int, total: int, batch: int,
+                 head0: int, head1: int, heads: int):
+        object.__setattr__(self, "_bank", bank)
+        object.__setattr__(self, "_range", (lo, hi, total, batch, head0, head1, heads))
+        for name in ("valid", "refreshed_at", "pending_stats", "pending_age"):
+            object.__setattr__(self, name, getattr(bank, name))
+
+    def __getattr__(self, name):
+        if name in BankChunk._TENSORS:
+            lo, hi, _, batch, h0, h1, _ = self._range
+            whole = getattr(self._bank, name)
+            if whole is None:
+                return None
+            if name == "partition":
+                return whole[batch:batch + 1, h0:h1]
+            return whole[lo:hi]
+        return getattr(self._bank, name)
+
+    def __setattr__(self, name, value):
+        if name not in BankChunk._TENSORS:
+            object.__setattr__(self, name, value)
+            return
+        lo, hi, total, batch, h0, h1, heads = self._range
+        if value is None:
+            setattr(self._bank, name, None)
+            return
+        whole = getattr(self._bank, name)
+        if name == "partition":
+            shape = (max(1, total // heads), heads, *value.shape[2:])
+        else:
+            shape = (total, *value.shape[1:])
+        if whole is None or tuple(whole.shape) != shape:
+            whole = torch.empty(shape, dtype=value.dtype, device=value.device)
+            setattr(self._bank, name, whole)
+        if name == "partition":
+            whole[batch:batch + 1, h0:h1] = value
+        else:
+            whole[lo:hi] = value
+
+    def commit(self, views: list["BankChunk"]) -> None:
+        bank = self._bank
+        bank.valid = self.valid
+        bank.refreshed_at = self.refreshed_at
+        bank.pending_age = self.pending_age
+        stats = [v.pending_stats for v in views if v.pending_stats is not None]
+        bank.pending_stats = None if not stats else (
+            stats[0] if len(stats) == 1 else torch.stack(stats).sum(dim=0))
+
+
+@dataclass
+class Operator:
+    """Dispatches one attention call per layer and owns the detail banks."""
+
+    config: OperatorConfig
+    layout: Layout
+    layers: list[list[SparseAttention]]
+    banks: list[list[DetailBank]] = field(default_factory=list)
+    kind: str = EXACT
+    step: int = 0
+    stream: int = 0
+    refreshed_layers: int = 0
+    alpha_override: float | None = None
+    #: when a dict, SPARSE calls record timing events after each stage (name -> events)
+    stage_events: dict | None = None
+    _chunk_states: dict = field(default_factory=dict)
+    _forced_partition: torch.Tensor | None = None
+    _forced_rerank: bool | None = None
+
+    def __post_init__(self) -> None:
+        if not self.layers or isinstance(self.layers[0], SparseAttention):
+            raise TypeError("Operator.layers must be indexed [stream][layer]")
+        self.banks = [[DetailBank() for _ in row] for row in self.layers]
+
+    @classmethod
+    def build(cls, config: OperatorConfig, geometry: SparseGeometry, *, n_layers: int,
+              n_streams: int = 1) -> "Operator":
+        if n_layers < 1 or n_streams < 1:
+            raise ValueError("n_layers and n_streams must be positive")
+        layers = [[SparseAttention(geometry, config) for _ in range(n_layers)]
+                  for _ in range(n_streams)]
+        return cls(config, geometry.layout, layers)
+
+    @property
+    def n_streams(self) -> int:
+        return len(self.layers)
+
+    def reset(self) -> None:
+        for row in self.banks:
+            for bank in row:
+                bank.release()
+        for row in self.layers:
+            for layer in row:
+                layer.reset()
+        self.kind = EXACT
+        self.step = 0
+        self.stream = 0
+        self.refreshed_layers = 0
+        for state in self._chunk_states.values():
+            state.reset()
+
+    @property
+    def banks_valid(self) -> bool:
+        return bool(self.banks) and all(bank.valid for row in self.banks for bank in row)
+
+    def begin_step(self, step: int, kind: str) -> None:
+        if kind not in (EXACT, REFRESH, SPARSE):
+            raise ValueError(f"unknown computed call kind {kind!r}")
+        self.step = int(step)
+        self.kind = kind
+        self.stream = 0
+        self.refreshed_layers = 0
+
+    def set_stream(self, stream: int) -> None:
+        if not 0 <= stream < self.n_streams:
+            raise ValueError(f"stream {stream} outside 0..{self.n_streams - 1}")
+        self.stream = int(stream)
+
+    # -- dispatch ------------------------------------------------------------------------
+
+    def _geometry(self, query: torch.Tensor) -> K.Geometry:
+        self.layout._check(query)
+        return K.Geometry(n_tokens=query.shape[-2], n_video=self.layout.video_tokens)
+
+    @torch.no_grad()
+    def attend(self, layer_index: int, query: torch.Tensor, key: torch.Tensor,
+               value: torch.Tensor) -> torch.Tensor:
+        """One attention call (recap/operator.py:233-258)."""
+        if self.kind == EXACT:
+            return F.scaled_dot_product_attention(query, key, value, dropout_p=0.0,
+                                                  is_causal=False)
+        if query.shape != key.shape or key.shape != value.shape:
+            raise ValueError("Q/K/V shapes differ")
+        chunks = int(self.config.bank_chunks)
+        if chunks > 1:
+            return self._attend_in_chunks(layer_index, query, key, value, chunks)
+        layer = self.layers[self.stream][layer_index]
+        bank = self.banks[self.stream][layer_index]
+        q, k, v = (K.prepare(x, n) for x, n in ((query, "query"), (key, "key"), (value, "value")))
+        geo = self._geometry(q)
+        rowmap = self.layout.rowmap(q.device)
+        if self.kind == SPARSE:
+            return self._sparse(layer, bank, q, k, v, geo, rowmap)
+        kv = K.kv_pack(k, v, rowmap, geo)
+        out, lse = K.dense_attn(q, kv, rowmap, K.scale_for(q.shape[-1]))
+        self._refresh(layer, bank, q, kv, geo, rowmap, out, lse)
+        return out
+
+    @torch.no_grad()
+    def _attend_in_chunks(self, layer_index, query, key, value, chunks):
+        """One layer in groups of heads (recap/operator.py:260-326); result-identical."""
+        b, h, n, d = query.shape
+        q, k, v = (K.prepare(x, n) for x, n in ((query, "query"), (key, "key"), (value, "value")))
+        geo = self._geometry(q)
+        rowmap = self.layout.rowmap(q.device)
+        bank = self.banks[self.stream][layer_index]
+        out = torch.empty(b, h, n, d, dtype=q.dtype, device=q.device)
+        lse = None
+        if self.kind == REFRESH:
+            kv_all = K.kv_pack(k, v, rowmap, geo)
+            _, lse = K.dense_attn(q, kv_all, rowmap, K.scale_for(d), out=out)
+            del kv_all
+        forced = None
+        if self.kind == REFRESH and bank.valid and bank.partition is not None:
+            layer0 = self.layers[self.stream][layer_index]
+            kv_all = K.kv_pack(k, v, rowmap, geo)
+            forced = layer0.head_partition(q, kv_all, rowmap, geo, K.scale_for(d))
+            del kv_all
+            kept, total = K.mask_overlap(forced, bank.partition)
+            self._forced_rerank = kept / max(total, 1) < self.config.rerank_min_overlap
+            forced = forced.reshape(b, h, geo.nb, geo.nb)
+        per = max(1, math.ceil(h / chunks))
+        views: list[BankChunk] = []
+        group = 0
+        refreshed_before = self.refreshed_layers
+        for bi in range(b):
+            for h0 in range(0, h, per):
+                h1 = min(h0 + per, h)
+                state = self._chunk_states.get((self.stream, layer_index, group))
+                if state is None:
+                    state = SparseAttention(self.layers[self.stream][layer_index].geometry,
+                                            self.config)
+                    self._chunk_states[(self.stream, layer_index, group)] = state
+                view = BankChunk(bank, lo=bi * h + h0, hi=bi * h + h1, total=b * h, batch=bi,
+                                 head0=h0, head1=h1, heads=h)
+                views.append(view)
+                qs, ks, vs = (x[bi:bi + 1, h0:h1] for x in (q, k, v))
+                self._forced_partition = (None if forced is None
+                                          else forced[bi:bi + 1, h0:h1].reshape(-1, geo.nb, geo.nb))
+                if self.kind == SPARSE:
+                    self._sparse(state, view, qs, ks, vs, geo, rowmap, out=out[bi:bi + 1, h0:h1])
+                else:
+                    kv = K.kv_pack(ks, vs, rowmap, geo)
+                    self._refresh(state, view, qs, kv, geo, rowmap, out[bi:bi + 1, h0:h1],
+                                  lse[bi:bi + 1, h0:h1])
+                group += 1
+        self._forced_partition = None
+        self._forced_rerank = None
+        if views:
+            views[-1].commit(views)
+        if self.refreshed_layers > refreshed_before:
+            self.refreshed_layers = refreshed_before + 1
+        return out
+
+    # -- refresh -------------------------------------------------------------------------
+
+    def _select(self, layer, q, kv, geo, rowmap):
+        b, h = q.shape[:2]
+        part = layer.head_partition(q, kv, rowmap, geo, K.scale_for(q.shape[-1]))
+        return part.reshape(b, h, geo.nb, geo.nb), K.kernel_block_mask(part, geo)
+
+    @torch.no_grad()
+    def _refresh(self, layer, bank, q, kv, geo, rowmap, full_output, full_lse) -> None:
+        """Store the refinement and measure the previous one (recap/operator.py:330-473)."""
+        b, h, n, d = q.shape
+        banks = b * h
+        scale = K.scale_for(d)
+        revalidating = bank.valid
+        if not revalidating:
+            bank.partition, bank.head_kernel_mask = self._select(layer, q, kv, geo, rowmap)
+        head_out, head_lse = K.block_sparse_attn(q, kv, rowmap, bank.head_kernel_mask, geo, scale)
+        context = layer.coarse_tail_context(kv, geo)
+        flat_part = bank.partition.reshape(banks, geo.nb, geo.nb)
+        old_lse = bank.coarse_lse if revalidating else None
+        go, gl, drift_part = layer.coarse_tail_apply(q, rowmap, context, flat_part, geo, scale,
+                                                     glref=old_lse)
+        if bank.value is None:
+            bank.value = torch.empty(banks, geo.rows, d, dtype=torch.float16, device=q.device)
+            bank.log_mass = torch.empty(banks, geo.rows, dtype=torch.float32, device=q.device)
+        center = K.drift_center(drift_part, geo) if old_lse is not None else None
+        stats = K.refresh_capture(full_output, full_lse, head_out, head_lse, go, gl, rowmap, geo,
+                                  bank.value, bank.log_mass, glref=old_lse, center=center)
+        if stats is not None:
+            bank.pending_stats = stats
+            bank.pending_age = self.step - bank.refreshed_at
+
+        if revalidating:
+            if self._forced_partition is not None:
+                partition = self._forced_partition.reshape(b, h, geo.nb, geo.nb)
+                kmask = K.kernel_block_mask(partition, geo)
+            else:
+                partition, kmask = self._select(layer, q, kv, geo, rowmap)
+            if bank.partition is not None:
+                if self._forced_rerank is None:
+                    kept, total = K.mask_overlap(partition, bank.partition)
+                    keep_split = kept / max(total, 1) >= self.config.rerank_min_overlap
+                else:
+                    keep_split = not self._forced_rerank
+                if keep_split:
+                    bank.coarse_lse = gl.clone()
+                    bank.refreshed_at = self.step
+                    bank.valid = True
+                    self.refreshed_layers += 1
+                    return
+            bank.partition, bank.head_kernel_mask = partition, kmask
+            head_out, head_lse = K.block_sparse_attn(q, kv, rowmap, bank.head_kernel_mask, geo,
+                                                     scale)
+            go, gl, _ = layer.coarse_tail_apply(
+                q, rowmap, context, bank.partition.reshape(banks, geo.nb, geo.nb), geo, scale)
+            K.refresh_capture(full_output, full_lse, head_out, head_lse, go, gl, rowmap, geo,
+                              bank.value, bank.log_mass)
+        bank.coarse_lse = gl.clone()
+        bank.refreshed_at = self.step
+        bank.valid = True
+        self.refreshed_layers += 1
+
+    # -- sparse --------------------------------------------------------------------------
+
+    @torch.no_grad()
+    def _sparse(self, layer, bank, q, k, v, geo, rowmap, out=None) -> torch.Tensor:
+        """Head exactly, plus coarse tail and weighted cached refinement
+        (recap/operator.py:477-527), as four launches with the merge fused."""
+        if not bank.valid or bank.head_kernel_mask is None:
+            raise RuntimeError("a sparse call was requested before an exact refresh")
+        b, h, n, d = q.shape
+        banks = b * h
+        scale = K.scale_for(d)
+        self._mark("start")
+        kv = K.kv_pack(k, v, rowmap, geo)
+        self._mark("pack")
+        context = layer.coarse_tail_context(kv, geo)
+        self._mark("closure")
+        old_lse = bank.coarse_lse
+        go, gl, drift_part = layer.coarse_tail_apply(
+            q, rowmap, context, bank.partition.reshape(banks, geo.nb, geo.nb), geo, scale,
+            glref=old_lse)
+        center = K.drift_center(drift_part, geo) if geo.rows else None
+        self._mark("coarse")
+        out = K.sparse_merge_attn(q, kv, rowmap, bank.head_kernel_mask, geo, scale, go, gl,
+                                  bank.value, bank.log_mass, old_lse, center,
+                                  alpha_override=self.alpha_override, out=out)
+        self._mark("attention")
+        return out
+
+    # -- the refinement error ------------------------------------------------------------
+
+    def drain_validation(self) -> tuple[int, float] | None:
+        """Relative RMS error over all layers and the smallest refinement age
+        (recap/operator.py:531-547)."""
+        stats, ages = [], []
+        for row in self.banks:
+            for bank in row:
+                if bank.pending_stats is not None and bank.pending_age is not None:
+                    stats.append(bank.pending_stats)
+                    ages.append(int(bank.pending_age))
+                bank.pending_stats = None
+                bank.pending_age = None
+        if not stats:
+            return None
+        numerator, denominator = (float(x) for x in torch.stack(stats).sum(dim=0))
+        error = math.sqrt(numerator / denominator) if denominator > 0.0 else float("inf")
+        return min(ages), error
+
+    def peak_bank_bytes(self) -> int:
+        total = 0
+        for row in self.banks:
+            for bank in row:
+                for tensor in (bank.value, bank.log_mass):
+                    if tensor is not None:
+                        total += tensor.numel() * tensor.element_size()
+        return total

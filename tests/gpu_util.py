@@ -1,0 +1,85 @@
+"""Helpers shared by the GPU parity tests."""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+import oracle as O
+from recap_amd.kernels import BLOCK
+from recap_amd.synthetic import Workload
+
+# Small shapes that still exercise every layout case the reference configurations have.
+SMALL = {
+    # the CPU-plumbing configuration's shape, bf16
+    "tiny": Workload("tiny", 2, 64, (4, 32, 32), 0, False, 0.25, torch.bfloat16),
+    # CogVideoX-like: text first, ragged last video block shared with text
+    "text-first-ragged": Workload("text-first-ragged", 2, 64, (3, 15, 25), 226, True, 0.25,
+                                  torch.bfloat16),
+    # HunyuanVideo-like: d=128, text last, ragged shared block
+    "text-last-d128": Workload("text-last-d128", 3, 128, (3, 15, 20), 256, False, 0.2,
+                               torch.bfloat16),
+    # Wan-like: d=128, video only, ragged last block
+    "video-ragged-d128": Workload("video-ragged-d128", 2, 128, (5, 10, 13), 0, False, 0.2,
+                                  torch.bfloat16, value_field=True),
+}
+
+
+def banks_view(x: torch.Tensor, fwd: torch.Tensor) -> torch.Tensor:
+    """Native [B, H, N, d] -> reordered [B*H, N, d] on the CPU."""
+    b, h, n, d = x.shape
+    return O.reorder(x.cpu(), fwd).reshape(b * h, n, d)
+
+
+def metrics(got: torch.Tensor, ref: torch.Tensor) -> tuple[float, float]:
+    g, r = got.double().flatten().cpu(), ref.double().flatten().cpu()
+    max_abs = float((g - r).abs().max())
+    cos = float(torch.dot(g, r) / (g.norm() * r.norm()).clamp_min(1e-300))
+    return max_abs, cos
+
+
+def assert_close_bf16(got, ref, what, max_abs=2e-2, cos=0.999):
+    m, c = metrics(got, ref)
+    print(f"[{what}] max_abs={m:.3e} cos={c:.6f}", flush=True)
+    assert m <= max_abs and c >= cos, f"{what}: max_abs={m} cos={c}"
+
+
+def k_tile_to_rows(tile: torch.Tensor, d: int) -> torch.Tensor:
+    """Undo the K tile image (chunk c of key row k at chunk c ^ (k % (d/8)))."""
+    nch = d // 8
+    img = tile.reshape(BLOCK, nch, 8)
+    out = torch.empty_like(img)
+    for key in range(BLOCK):
+        for c in range(nch):
+            out[key, c] = img[key, c ^ (key % nch)]
+    return out.reshape(BLOCK, d)
+
+
+def vt_tile_to_rows(tile: torch.Tensor, d: int) -> torch.Tensor:
+    """Undo the V^T tile image: row d, chunk c at c ^ (d % 16); position p holds key
+    swap23(p).  Returns V rows [128, d]."""
+    img = tile.reshape(d, 16, 8)
+    vt = torch.empty(d, BLOCK, dtype=tile.dtype)
+    for row in range(d):
+        for c in range(16):
+            vt[row, 8 * c:8 * c + 8] = img[row, c ^ (row % 16)]
+    keys = [(p & ~12) | ((p & 4) << 1) | ((p & 8) >> 1) for p in range(BLOCK)]
+    out = torch.empty(BLOCK, d, dtype=tile.dtype)
+    out[keys] = vt.T
+    return out
+
+
+def video_query_blocks(n_video: int, count: int, seed: int = 0) -> list[int]:
+    """A spread-out subset of query blocks (always including the first and last)."""
+    rows = n_video // BLOCK
+    if rows <= count:
+        return list(range(rows))
+    rng = np.random.default_rng(seed)
+    pick = set(rng.choice(rows, size=count - 2, replace=False).tolist()) | {0, rows - 1}
+    return sorted(pick)
+
+
+def scale_for(d: int) -> float:
+    return 1.0 / math.sqrt(d)

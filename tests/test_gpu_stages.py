@@ -1,0 +1,180 @@
+"""GPU parity of each HIP stage against the CPU oracle, on the same seeded inputs.
+
+Masks, pooled means and block scores must be bit-exact; bf16 outputs within max-abs
+2e-2 and cosine >= 0.999; fp32 statistics within the tolerance stated per test."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_util import (SMALL, assert_close_bf16, banks_view, k_tile_to_rows, metrics,
+                      scale_for, vt_tile_to_rows)
+from recap_amd import _lib
+from recap_amd import kernels as K
+from recap_amd.layout import Layout, hilbert_permutation
+from recap_amd.synthetic import WORKLOADS, make_qkv
+
+pytestmark = pytest.mark.gpu
+
+STAGE1_CASES = [("tiny", None), ("text-first-ragged", None), ("text-last-d128", None),
+                ("video-ragged-d128", None), ("wan2.1-480p", [0, 5]), ("cogvideox1.5", [0, 7]),
+                ("hunyuan-720p", [0, 1])]
+
+
+def _setup(name, heads, cuda, seed=0, dtype=None):
+    wl = SMALL.get(name) or WORKLOADS[name]
+    dtype = dtype or (torch.bfloat16 if wl.dtype == torch.float32 else wl.dtype)
+    print(f"case {name} heads={heads} N={wl.tokens} d={wl.dim}", flush=True)
+    q, k, v = make_qkv(wl, heads=heads, seed=seed, dtype=dtype)
+    perm = hilbert_permutation(wl.grid)
+    layout = Layout.from_permutation(perm, text_tokens=wl.text_tokens, text_first=wl.text_first)
+    fwd, _ = O.gather_indices(perm, wl.text_tokens, wl.text_first)
+    geo = K.Geometry(wl.tokens, wl.video_tokens)
+    return wl, (q, k, v), tuple(x.to(cuda) for x in (q, k, v)), layout.rowmap(cuda), fwd, geo
+
+
+@pytest.mark.parametrize("name,heads", STAGE1_CASES)
+def test_stage1_pool_scores_masks_bit_exact(cuda, name, heads):
+    wl, (q, k, v), (qg, kg, vg), rowmap, fwd, geo = _setup(name, heads, cuda)
+    ql, kl = banks_view(q, fwd), banks_view(k, fwd)
+    kv = K.kv_pack(kg, vg, rowmap, geo)
+    qm = K.pool_blocks(qg, rowmap, geo)
+    qm_ref, _ = O.pool_blocks(ql, wl.video_tokens)
+    km_ref, _ = O.pool_blocks(kl, wl.video_tokens)
+    assert torch.equal(qm.cpu().view(torch.int32), qm_ref.view(torch.int32))
+    assert torch.equal(kv.k_means.cpu().view(torch.int32), km_ref.view(torch.int32))
+    vm_ref, _ = O.pool_blocks(banks_view(v, fwd), wl.video_tokens)
+    assert torch.equal(kv.v_means.cpu().view(torch.int32), vm_ref.view(torch.int32))
+    scale = scale_for(wl.dim)
+    scores = K.block_scores(qm, kv.k_means, scale)
+    scores_ref = O.block_scores(qm_ref, km_ref, scale)
+    assert torch.equal(scores.cpu().view(torch.int32), scores_ref.view(torch.int32))
+    part = K.select_blocks(qg, kv.k_means, rowmap, geo, wl.density, scale)
+    part_ref = O.head_partition(ql, kl, scale, wl.density, wl.video_tokens)
+    keep = max(1, round(wl.density * geo.nb))
+    print(f"  top-k margin {O.topk_margin(scores_ref, keep):.3e}", flush=True)
+    assert torch.equal(part.cpu(), part_ref)
+    kmask = K.kernel_block_mask(part, geo)
+    assert torch.equal(kmask.cpu(), O.kernel_block_mask(part_ref, wl.tokens, wl.video_tokens))
+
+
+@pytest.mark.parametrize("name", list(SMALL))
+def test_kv_pack_tile_images(cuda, name):
+    wl, (q, k, v), (qg, kg, vg), rowmap, fwd, geo = _setup(name, None, cuda)
+    kv = K.kv_pack(kg, vg, rowmap, geo)
+    kl, vl = banks_view(k, fwd), banks_view(v, fwd)
+    kt, vt = kv.k_tiles.cpu(), kv.vt_tiles.cpu()
+    n = wl.tokens
+    for bank in range(kl.shape[0]):
+        for tile in sorted({0, geo.tb // 2, geo.tb - 1}):
+            rows = min(128, n - 128 * tile)
+            krows = k_tile_to_rows(kt[bank, tile], wl.dim)
+            vrows = vt_tile_to_rows(vt[bank, tile], wl.dim)
+            assert torch.equal(krows[:rows], kl[bank, 128 * tile:128 * tile + rows])
+            assert torch.equal(vrows[:rows], vl[bank, 128 * tile:128 * tile + rows])
+            assert not krows[rows:].any() and not vrows[rows:].any()
+
+
+@pytest.mark.parametrize("name", list(SMALL))
+def test_head_and_dense_attention(cuda, name):
+    wl, (q, k, v), (qg, kg, vg), rowmap, fwd, geo = _setup(name, None, cuda)
+    scale = scale_for(wl.dim)
+    kv = K.kv_pack(kg, vg, rowmap, geo)
+    ql, kl, vl = (banks_view(x, fwd) for x in (q, k, v))
+    part_ref = O.head_partition(ql, kl, scale, wl.density, wl.video_tokens)
+    kmask_ref = O.kernel_block_mask(part_ref, wl.tokens, wl.video_tokens)
+    out, lse = K.block_sparse_attn(qg, kv, rowmap, kmask_ref.to(cuda), geo, scale)
+    ref, ref_lse = O.block_sparse_attention(ql, kl, vl, kmask_ref, scale)
+    assert_close_bf16(out.cpu().float(), ref, f"head {name}")
+    m, _ = metrics(lse.cpu(), ref_lse)
+    assert m < 2e-3, m
+    dense, dlse = K.dense_attn(qg, kv, rowmap, scale)
+    dref, dref_lse = O.dense_attention(ql, kl, vl, scale)
+    _, inv = O.gather_indices(hilbert_permutation(wl.grid), wl.text_tokens, wl.text_first)
+    b, h = q.shape[:2]
+    assert_close_bf16(dense.cpu().float(), O.restore(dref.reshape(b, h, -1, wl.dim), inv),
+                      f"dense {name}")
+    m, _ = metrics(dlse.cpu(), dref_lse.reshape(b, h, -1).index_select(-1, inv))
+    assert m < 2e-3, m
+
+
+def test_dense_attention_matches_torch_sdpa(cuda):
+    wl = SMALL["text-last-d128"]
+    q, k, v = (x.to(cuda) for x in make_qkv(wl, seed=1))
+    layout = Layout.from_permutation(hilbert_permutation(wl.grid), text_tokens=wl.text_tokens,
+                                     text_first=False)
+    rowmap = layout.rowmap(cuda)
+    geo = K.Geometry(wl.tokens, wl.video_tokens)
+    kv = K.kv_pack(k, v, rowmap, geo)
+    out, _ = K.dense_attn(q, kv, rowmap, scale_for(wl.dim))
+    ref = torch.nn.functional.scaled_dot_product_attention(q.float(), k.float(), v.float())
+    assert_close_bf16(out.float(), ref, "dense vs sdpa fp32")
+
+
+@pytest.mark.parametrize("name", ["tiny", "text-last-d128", "video-ragged-d128"])
+def test_closure_statistics(cuda, name):
+    wl, (q, k, v), (qg, kg, vg), rowmap, fwd, geo = _setup(name, None, cuda)
+    kv = K.kv_pack(kg, vg, rowmap, geo)
+    kl, vl = banks_view(k, fwd), banks_view(v, fwd)
+    km_ref, counts = O.pool_blocks(kl, wl.video_tokens)
+    _, cvk, scatter = K.closure_stats(kv, geo, _lib.CLOSURE_CVK | _lib.CLOSURE_SCATTER)
+    scatter_ref = O.within_block_scatter(kl, km_ref, counts, wl.video_tokens)
+    cvk_ref = O.value_key_covariance(kl, vl, km_ref, counts, wl.video_tokens)
+    rel = float((scatter.cpu() - scatter_ref).abs().max() / scatter_ref.abs().max())
+    print(f"  scatter rel {rel:.2e}", flush=True)
+    assert rel < 1e-4
+    m, c = metrics(cvk.cpu(), cvk_ref)
+    print(f"  cvk max_abs {m:.2e} cos {c:.6f}", flush=True)
+    assert m < 1e-4 * max(1.0, float(cvk_ref.abs().max()))
+    basis = O.closure_basis(scatter_ref)
+    split = K.basis_tables(basis.to(cuda), None, kv.dtype, split=True)
+    var, cvk2, _ = K.closure_stats(kv, geo, _lib.CLOSURE_ROT | _lib.CLOSURE_CVK, split.u_hi_t,
+                                   split.u_lo_t)
+    assert torch.equal(cvk2, cvk)
+    var_only, _, _ = K.closure_stats(kv, geo, _lib.CLOSURE_ROT, split.u_hi_t, split.u_lo_t)
+    assert torch.equal(var_only, var)
+    _, var_ref = O.rotated_moments(kl, basis, counts, wl.video_tokens)
+    rel = float(((var.cpu() - var_ref).abs() / (var_ref.abs() + 1e-3)).max())
+    print(f"  rotated variance rel {rel:.2e}", flush=True)
+    assert rel < 1e-3
+
+
+@pytest.mark.parametrize("name", ["tiny", "text-first-ragged", "text-last-d128",
+                                  "video-ragged-d128"])
+def test_coarse_tail(cuda, name):
+    """The coarse kernel against the oracle fed with the same closure statistics."""
+    wl, (q, k, v), (qg, kg, vg), rowmap, fwd, geo = _setup(name, None, cuda)
+    scale = scale_for(wl.dim)
+    kv = K.kv_pack(kg, vg, rowmap, geo)
+    ql, kl, vl = (banks_view(x, fwd) for x in (q, k, v))
+    km_ref, counts = O.pool_blocks(kl, wl.video_tokens)
+    vm_ref, _ = O.pool_blocks(vl, wl.video_tokens)
+    scatter = O.within_block_scatter(kl, km_ref, counts, wl.video_tokens)
+    basis = O.closure_basis(scatter)
+    _, var = O.rotated_moments(kl, basis, counts, wl.video_tokens)
+    basis, var = O.order_basis(basis, var, counts)
+    cvk = O.value_key_covariance(kl, vl, km_ref, counts, wl.video_tokens)
+    w = O.fold_rank(var, 4)
+    part = O.head_partition(ql, kl, scale, wl.density, wl.video_tokens)
+    qv = ql[:, :wl.video_tokens].float()
+    qsq = O.rotated_query_square(qv, basis, torch.bfloat16)
+    drift = O.value_drift(qv, cvk, scale, torch.bfloat16)
+    go_ref, gl_ref = O.coarse_tail(ql, qsq, drift, km_ref, vm_ref, w, counts, part, scale, 2.0,
+                                   wl.video_tokens, torch.bfloat16)
+    rows = geo.rows
+    qt = K.basis_tables(basis.to(cuda), cvk.to(cuda), kv.dtype, query=True, cvk_table=True)
+    wt, kbar, vbar = K.coarse_tables(var.to(cuda), kv, 4)
+    tables = {"w": wt, "kbar": kbar, "vbar": vbar, "u_t": qt.u_t, "cvk_t": qt.cvk_t}
+    glref = torch.randn(kl.shape[0], rows, generator=torch.Generator().manual_seed(3)).to(cuda)
+    go, gl, dpart = K.coarse_tail(qg, rowmap, part.to(cuda), geo, tables, scale, 2.0, glref)
+    assert_close_bf16(go.cpu().float(), go_ref[:, :rows], f"coarse {name}")
+    fin = torch.isfinite(gl_ref[:, :rows])
+    assert torch.equal(torch.isfinite(gl.cpu()), fin)
+    m, _ = metrics(gl.cpu()[fin], gl_ref[:, :rows][fin])
+    assert m < 2e-3, m
+    center = K.drift_center(dpart, geo)
+    cref = O.drift_center(gl.cpu(), glref.cpu())
+    assert torch.allclose(center.cpu(), cref, atol=1e-4, rtol=1e-4)

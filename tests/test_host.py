@@ -1,0 +1,168 @@
+"""Host-side checks that need no GPU: the C ABI library loads and exports every symbol
+the header declares, host-only entry points, argument validation, config and layout."""
+
+import ctypes
+import json
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from recap_amd import _lib, config as C, kernels as K
+from recap_amd.layout import Layout, SparseGeometry, hilbert_permutation
+from recap_amd.synthetic import WORKLOADS
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "recap_hip.h"
+
+
+def declared_symbols() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(recap_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_symbols()
+    assert len(names) >= 20
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(_lib.SIGNATURES)
+    assert lib.recap_abi_version() == _lib.ABI_VERSION
+
+
+@pytest.mark.parametrize("name", list(WORKLOADS))
+def test_native_hilbert_matches_oracle(name):
+    grid = WORKLOADS[name].grid
+    np.testing.assert_array_equal(hilbert_permutation(grid), O.hilbert_permutation(grid))
+
+
+@pytest.mark.parametrize("grid", [(1, 1, 1), (1, 1, 7), (3, 5, 2), (2, 16, 16)])
+def test_native_hilbert_small_grids(grid):
+    np.testing.assert_array_equal(hilbert_permutation(grid), O.hilbert_permutation(grid))
+
+
+def test_argument_validation_before_launch():
+    # Every check below fires on the host before any HIP call.
+    with pytest.raises(ValueError, match="head dim"):
+        _lib.call("recap_pool_blocks", 16, _lib.RECAP_BF16, 1, 1, 96, 0, 0, 96, 16, 256, 256, 16,
+                  None)
+    with pytest.raises(ValueError, match="dtype"):
+        _lib.call("recap_pool_blocks", 16, 7, 1, 1, 64, 0, 0, 64, 16, 256, 256, 16, None)
+    with pytest.raises(ValueError, match="16-byte"):
+        _lib.call("recap_pool_blocks", 18, _lib.RECAP_BF16, 1, 1, 64, 0, 0, 64, 16, 256, 256, 16,
+                  None)
+    with pytest.raises(ValueError, match="n_tokens"):
+        _lib.call("recap_kv_pack", 16, 16, _lib.RECAP_BF16, 1, 1, 64, 0, 0, 64, 0, 0, 64, 16,
+                  100, 200, 16, 16, 16, 16, None)
+    with pytest.raises(ValueError, match="keep"):
+        _lib.call("recap_topk_blocks", 16, 1, 10, 11, 0, 16, None)
+    with pytest.raises(ValueError, match="flag"):
+        _lib.call("recap_closure_stats", 16, 16, 16, _lib.RECAP_BF16, 16, 16, 1, 64, 256, 256, 8,
+                  _lib.CLOSURE_SCATTER, 16, 16, 16, None)
+    with pytest.raises(ValueError, match="drift weight"):
+        _lib.call("recap_sparse_merge_attn", 16, _lib.RECAP_BF16, 1, 1, 64, 0, 0, 64, 16, 16, 16,
+                  16, 256, 256, 0.125, 16, 16, 16, 16, None, None, -1.0, 16, 0, 0, 64, None)
+    with pytest.raises(ValueError, match="kernel blocks"):
+        _lib.call("recap_dense_attn", 16, _lib.RECAP_BF16, 1, 1, 64, 0, 0, 64, 16, 16, 16,
+                  2049 * 128, 0.125, 16, 0, 0, 64, 16, None)
+
+
+def test_workspace_queries():
+    lib = _lib.load()
+    assert lib.recap_closure_groups(118800, 8) == 117
+    assert lib.recap_closure_groups(0, 8) == -1
+    assert lib.recap_capture_partials(24, 128, 118800) == 24 * 118784 // 16
+    assert lib.recap_capture_partials(2, 64, 4096) == 2 * 4096 // 32
+
+
+def test_geometry_matches_reference_shapes():
+    hun = K.Geometry(119056, 118800)
+    assert (hun.nb, hun.tb, hun.ds, hun.rows) == (929, 931, 928, 118784)
+    cog = K.Geometry(45106, 44880)
+    assert (cog.nb, cog.tb, cog.ds, cog.rows) == (351, 353, 350, 44800)
+    wan = K.Geometry(32760, 32760)
+    assert (wan.nb, wan.tb, wan.ds, wan.rows) == (256, 256, 256, 32640)
+    assert wan.counts("cpu")[-1] == 120
+
+
+def test_xcd_linear_is_a_bijection():
+    # Host restatement of the device work-item remap in csrc/common.hpp.
+    for n in (1, 7, 8, 9, 22344, 931 * 24 + 5):
+        seen = set()
+        for bid in range(n):
+            xcd, slot = bid & 7, bid >> 3
+            per, rem = n >> 3, n & 7
+            seen.add(xcd * per + min(xcd, rem) + slot)
+        assert seen == set(range(n))
+
+
+def test_layout_rowmap_and_round_trip():
+    perm = hilbert_permutation((2, 8, 8))
+    for text_first in (False, True):
+        layout = Layout.from_permutation(perm, text_tokens=9, text_first=text_first)
+        fwd, inv = O.gather_indices(perm, 9, text_first)
+        assert torch.equal(layout.rowmap("cpu").long(), fwd)
+        x = torch.randn(1, 2, 137, 4)
+        assert torch.equal(layout.restore(layout.reorder(x)), x)
+        with pytest.raises(ValueError):
+            layout.reorder(torch.randn(1, 2, 100, 4))
+    geo = SparseGeometry.build(Layout.from_permutation(perm, text_tokens=0, text_first=False), 128)
+    assert geo.n_blocks == 1 and geo.block_counts.tolist() == [128.0]
+
+
+def test_config_loader_and_profiles(tmp_path):
+    for model in C.MODELS:
+        for preset in C.PRESETS:
+            raw = {"model": model, "preset": preset,
+                   "operating_point": {"B": 20, "tau_pred": 0.1, "tau_detail": 0.2}}
+            path = tmp_path / f"{model}_{preset}.json"
+            path.write_text(json.dumps(raw))
+            cfg = C.load_config(path)
+            assert cfg.schedule.budget == 20
+            assert cfg.schedule.detail_tau_mult == pytest.approx(2.0)
+            assert cfg.operating_point.tau_detail == pytest.approx(0.2)
+    cfg = C.config_from_dict({"model": "hunyuan", "preset": "fast",
+                              "operating_point": {"B": 17, "tau_pred": 0.2, "tau_detail": 0.2}})
+    assert cfg.operator.head_density == 0.2 and cfg.operator.bank_chunks == 4
+    assert cfg.geometry.grid == (33, 45, 80) and cfg.operator.host_banks
+    bad = [
+        ({"model": "x", "preset": "fast", "operating_point": {"B": 5, "tau_pred": 1, "tau_detail": 1}}, "unsupported"),
+        ({"model": "hunyuan", "preset": "fast", "operating_point": {"B": 2, "tau_pred": 1, "tau_detail": 1}}, "at least 3"),
+        ({"model": "hunyuan", "preset": "fast", "operating_point": {"B": 99, "tau_pred": 1, "tau_detail": 1}}, "num_steps"),
+        ({"model": "hunyuan", "preset": "fast", "operating_point": {"B": 5, "tau_pred": 1}}, "exactly"),
+        ({"model": "hunyuan", "preset": "fast", "extra": 1, "operating_point": {"B": 5, "tau_pred": 1, "tau_detail": 1}}, "unknown"),
+    ]
+    for raw, msg in bad:
+        with pytest.raises(ValueError, match=msg):
+            C.config_from_dict(raw)
+    for field, value in [("head_density", 1.0), ("closure_gate_theta", 0.0), ("closure_rank", -1),
+                         ("rerank_min_overlap", 1.5), ("bank_chunks", 0)]:
+        with pytest.raises(ValueError):
+            C.OperatorConfig(**{field: value}).validate()
+    with pytest.raises(ValueError, match="128"):
+        C.GeometryConfig(grid=(1, 2, 3), block_size=64).validate()
+
+
+def test_operator_host_errors():
+    from recap_amd.operator import Operator, REFRESH
+    from recap_amd.config import OperatorConfig
+    layout = Layout.from_permutation(hilbert_permutation((2, 8, 8)), text_tokens=0, text_first=False)
+    geo = SparseGeometry.build(layout, 128)
+    op = Operator.build(OperatorConfig(head_density=0.5), geo, n_layers=2, n_streams=2)
+    with pytest.raises(ValueError, match="kind"):
+        op.begin_step(0, "bogus")
+    with pytest.raises(ValueError, match="stream"):
+        op.set_stream(2)
+    with pytest.raises(ValueError):
+        Operator.build(OperatorConfig(), geo, n_layers=0)
+    op.begin_step(3, REFRESH)
+    assert op.kind == REFRESH and op.step == 3 and not op.banks_valid
+    assert op.drain_validation() is None and op.peak_bank_bytes() == 0
+    with pytest.raises(ValueError, match="GPU"):
+        op.attend(0, torch.zeros(1, 1, 128, 64, dtype=torch.bfloat16),
+                  torch.zeros(1, 1, 128, 64, dtype=torch.bfloat16),
+                  torch.zeros(1, 1, 128, 64, dtype=torch.bfloat16))

@@ -1,0 +1,395 @@
+"""Pins the CPU oracle: golden vectors from the reference, brute force on tiny inputs,
+closed forms and invariants.  Each check is chosen so that a plausible slip (a swapped
+axis, a wrong pairing in a reduction, a dropped term) fails it."""
+
+import hashlib
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from recap_amd.synthetic import WORKLOADS, make_qkv
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def sha(a: np.ndarray) -> str:
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+@pytest.fixture(scope="module")
+def golden():
+    meta = json.loads((GOLDEN / "golden.json").read_text())
+    arrays = np.load(GOLDEN / "golden.npz")
+    return meta, arrays
+
+
+# -- layout --------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("name", list(WORKLOADS))
+def test_hilbert_matches_reference_golden(golden, name):
+    meta, arrays = golden
+    perm = O.hilbert_permutation(WORKLOADS[name].grid).astype(np.int64)
+    assert sha(perm) == meta["hilbert"][name]["sha256_int64"]
+    if f"hilbert_{name}" in arrays:
+        np.testing.assert_array_equal(perm, arrays[f"hilbert_{name}"])
+
+
+def test_hilbert_is_a_continuous_curve_on_a_cube():
+    # On a 2^b cube consecutive Hilbert points are grid neighbours.
+    perm = O.hilbert_permutation((8, 8, 8))
+    assert np.unique(perm).size == 512
+    t, y, x = perm // 64, (perm // 8) % 8, perm % 8
+    steps = np.abs(np.diff(t)) + np.abs(np.diff(y)) + np.abs(np.diff(x))
+    assert np.all(steps == 1)
+
+
+def test_hilbert_blocks_are_compact():
+    grid = (4, 32, 32)
+    perm = O.hilbert_permutation(grid)
+    t, y, x = perm // 1024, (perm // 32) % 32, perm % 32
+    for b in range(perm.size // 128):
+        sl = slice(128 * b, 128 * (b + 1))
+        box = (np.ptp(t[sl]) + 1) * (np.ptp(y[sl]) + 1) * (np.ptp(x[sl]) + 1)
+        assert box <= 4 * 128  # a raster order would span whole rows (box >= 4*4*32)
+
+
+@pytest.mark.parametrize("text_first", [False, True])
+def test_gather_indices_round_trip(text_first):
+    perm = O.hilbert_permutation((2, 4, 8))
+    fwd, inv = O.gather_indices(perm, 5, text_first)
+    nv = perm.size
+    x = torch.arange(nv + 5, dtype=torch.float32).reshape(1, -1, 1)
+    xr = O.reorder(x, fwd)
+    assert torch.equal(O.restore(xr, inv), x)
+    video = xr[0, :nv, 0].long()
+    text = xr[0, nv:, 0].long()
+    off = 5 if text_first else 0
+    assert torch.equal(video, torch.as_tensor(perm) + off)
+    assert torch.equal(text, torch.arange(5) + (0 if text_first else nv))
+
+
+# -- stage 1 ----------------------------------------------------------------------------------
+
+
+def _pool_by_loops(x: np.ndarray, n_video: int) -> np.ndarray:
+    """Independent scalar restatement of the fixed pooling order."""
+    n, d = x.shape
+    lanes = 2048 // d
+    passes = 128 // lanes
+    nb = (n_video + 127) // 128
+    out = np.zeros((nb, d), dtype=np.float32)
+    for b in range(nb):
+        count = min(128, n_video - 128 * b)
+        for c in range(d):
+            part = []
+            for lane in range(lanes):
+                acc = None
+                for p in range(passes):
+                    t = 128 * b + lane + lanes * p
+                    v = np.float32(x[t, c]) if t < n_video else np.float32(0.0)
+                    acc = v if acc is None else np.float32(acc + v)
+                part.append(acc)
+            h = lanes // 2
+            while h >= 1:
+                part = [np.float32(part[i] + part[i + h]) for i in range(h)]
+                h //= 2
+            out[b, c] = np.float32(part[0] / np.float32(count))
+    return out
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_pool_blocks_fixed_order_and_mean(d):
+    g = torch.Generator().manual_seed(3)
+    nv = 300  # two full blocks and a 44-token tail
+    x = torch.randn(nv + 20, d, generator=g).to(torch.bfloat16)
+    mean, counts = O.pool_blocks(x.unsqueeze(0), nv)
+    assert counts.tolist() == [128.0, 128.0, 44.0]
+    ref = _pool_by_loops(x.float().numpy(), nv)
+    assert np.array_equal(mean[0].numpy().view(np.uint32), ref.view(np.uint32))
+    exact = torch.stack([x[i * 128:min(nv, (i + 1) * 128)].double().mean(0) for i in range(3)])
+    assert torch.allclose(mean[0].double(), exact, atol=1e-6, rtol=0)
+
+
+def test_block_scores_fixed_order():
+    g = torch.Generator().manual_seed(4)
+    qm = torch.randn(1, 5, 64, generator=g)
+    km = torch.randn(1, 7, 64, generator=g)
+    s = O.block_scores(qm, km, 0.125)
+    for i in range(5):
+        for j in range(7):
+            acc = np.float32(qm[0, i, 0] * km[0, j, 0])
+            for c in range(1, 64):
+                acc = np.float32(acc + np.float32(qm[0, i, c] * km[0, j, c]))
+            assert s[0, i, j].item() == np.float32(acc * np.float32(0.125))
+    assert torch.allclose(s.double(), (qm.double() @ km.double().transpose(-1, -2)) * 0.125,
+                          atol=1e-5)
+
+
+def test_topk_mask_brute_force_with_ties():
+    g = torch.Generator().manual_seed(5)
+    scores = torch.randn(3, 10, 17, generator=g)
+    scores[0, 0, 3] = scores[0, 0, 9] = scores[0, 0, 12] = 5.0  # tie at the top
+    scores[1, 2, :] = 1.0  # a fully tied row
+    mask = O.topk_mask(scores, 4)
+    for b in range(3):
+        for i in range(10):
+            order = sorted(range(17), key=lambda j: (-scores[b, i, j].item(), j))
+            expect = set(order[:4])
+            assert set(torch.nonzero(mask[b, i]).flatten().tolist()) == expect
+
+
+@pytest.mark.parametrize("name", list(WORKLOADS))
+def test_head_partition_matches_reference_golden(golden, name):
+    meta, arrays = golden
+    info = meta["masks"][name]
+    wl = WORKLOADS[name]
+    q, k, _ = make_qkv(wl, heads=info["heads"], seed=0)
+    fwd, _ = O.gather_indices(O.hilbert_permutation(wl.grid), wl.text_tokens, wl.text_first)
+    ql, kl = O.reorder(q, fwd)[0], O.reorder(k, fwd)[0]
+    part = O.head_partition(ql, kl, 1.0 / math.sqrt(wl.dim), wl.density, wl.video_tokens)
+    assert sha(part.numpy().astype(np.uint8)) == info["partition_sha256_u8"]
+    kmask = O.kernel_block_mask(part, wl.tokens, wl.video_tokens)
+    assert sha(kmask.numpy().astype(np.uint8)) == info["kernel_mask_sha256_u8"]
+    key = f"partition_{name}"
+    if key in arrays:
+        ref = np.unpackbits(arrays[key])[:part.numel()].reshape(part.shape).astype(bool)
+        np.testing.assert_array_equal(part.numpy(), ref)
+    counts = part.sum(-1)
+    if wl.video_tokens % 128:
+        assert part[..., -1].all() and part[..., -1, :].all()
+        assert counts[..., :-1].min() >= info["keep"] and counts[..., :-1].max() <= info["keep"] + 1
+    else:
+        assert (counts == info["keep"]).all()
+
+
+def test_kernel_block_mask_closed_form():
+    part = torch.zeros(1, 4, 4, dtype=torch.bool)
+    part[0, 1, 2] = True
+    # shared boundary block: video 3*128+5 tokens followed by text
+    m = O.kernel_block_mask(part, 3 * 128 + 5 + 200, 3 * 128 + 5)
+    assert m.shape == (1, 5, 5)  # 589 tokens, 4 video blocks (the last holds 5)
+    assert m[0, 3:, :].all() and m[0, :, 3:].all()
+    assert m[0, 1, 2] and not m[0, 0, 0] and not m[0, 2, 1]
+    # video-only, exact multiple: nothing forced
+    m2 = O.kernel_block_mask(part, 512, 512)
+    assert torch.equal(m2, part)
+
+
+# -- stage 2 ----------------------------------------------------------------------------------
+
+
+def test_block_sparse_attention_is_masked_softmax():
+    g = torch.Generator().manual_seed(6)
+    n, d = 300, 64  # ragged: 3 blocks, last one 44 tokens
+    q, k, v = (torch.randn(2, n, d, generator=g) for _ in range(3))
+    kmask = torch.rand(2, 3, 3, generator=g) > 0.4
+    kmask[:, :, 0] = True
+    out, lse = O.block_sparse_attention(q, k, v, kmask, 0.125)
+    tok = torch.arange(n) // 128
+    for b in range(2):
+        allowed = kmask[b][tok][:, tok]
+        s = (q[b].double() @ k[b].double().T) * 0.125
+        s = s.masked_fill(~allowed, -math.inf)
+        ref = torch.softmax(s, -1) @ v[b].double()
+        assert torch.allclose(out[b].double(), ref, atol=1e-5)
+        assert torch.allclose(lse[b].double(), torch.logsumexp(s, -1), atol=1e-5)
+
+
+# -- stage 3 ----------------------------------------------------------------------------------
+
+
+def _tiny_closure_inputs(seed=7, nv=300, d=64):
+    g = torch.Generator().manual_seed(seed)
+    k = (torch.randn(1, nv, d, generator=g) * torch.linspace(0.2, 2.0, d)).to(torch.bfloat16)
+    v = torch.randn(1, nv, d, generator=g).to(torch.bfloat16)
+    geo = O.block_geometry(nv, nv)
+    km, counts = O.pool_blocks(k, nv)
+    return k, v, km, counts, geo
+
+
+def test_within_block_scatter_direct():
+    k, _, km, counts, _ = _tiny_closure_inputs()
+    s = O.within_block_scatter(k, km, counts, 300)
+    ref = torch.zeros(64, 64, dtype=torch.float64)
+    for b in range(3):
+        blk = k[0, 128 * b:min(300, 128 * (b + 1))].double() - km[0, b].double()
+        ref += blk.T @ blk
+    assert torch.allclose(s[0].double(), ref / 300, atol=1e-5)
+
+
+def test_rotated_moments_rotation_and_sign_invariance():
+    k, _, km, counts, _ = _tiny_closure_inputs()
+    basis = O.closure_basis(O.within_block_scatter(k, km, counts, 300))
+    mean, var = O.rotated_moments(k, basis, counts, 300)
+    for b in range(3):
+        blk = k[0, 128 * b:min(300, 128 * (b + 1))].double()
+        trace = ((blk - blk.mean(0)) ** 2).sum(1).mean()
+        assert abs(var[0, b].double().sum() - trace) / trace < 2e-4
+    flipped = basis.clone()
+    flipped[..., ::3] *= -1
+    _, var2 = O.rotated_moments(k, flipped, counts, 300)
+    assert torch.allclose(var, var2, rtol=1e-6, atol=1e-7)
+    assert torch.allclose(mean[0, 0, ::3], -O.rotated_moments(k, flipped, counts, 300)[0][0, 0, ::3],
+                          atol=1e-6)
+
+
+def test_value_key_covariance_direct():
+    k, v, km, counts, _ = _tiny_closure_inputs()
+    c = O.value_key_covariance(k, v, km, counts, 300)
+    ref = torch.zeros(64, 64, dtype=torch.float64)
+    for b in range(3):
+        sl = slice(128 * b, min(300, 128 * (b + 1)))
+        ref += v[0, sl].double().T @ (k[0, sl].double() - km[0, b].double())
+    assert torch.allclose(c[0].double(), ref / 300, atol=1e-5)
+
+
+def test_fold_rank_and_order_basis():
+    g = torch.Generator().manual_seed(8)
+    var = torch.rand(2, 5, 16, generator=g)
+    w = O.fold_rank(var, 4)
+    assert torch.allclose(w.sum(-1), var.sum(-1), atol=1e-5)
+    assert torch.equal(w[..., :4], var[..., :4])
+    assert torch.allclose(w[..., 4:], var[..., 4:].mean(-1, keepdim=True).expand(-1, -1, 12))
+    basis = torch.linalg.qr(torch.randn(2, 16, 16, generator=g))[0]
+    counts = torch.tensor([128.0, 128.0, 128.0, 128.0, 7.0])
+    b2, v2 = O.order_basis(basis, var, counts)
+    pooled = (v2 * counts.view(1, -1, 1)).sum(1)
+    assert torch.all(pooled[:, :-1] >= pooled[:, 1:])
+    for bank in range(2):
+        for c in range(16):
+            col = torch.nonzero(torch.all(basis[bank] == b2[bank][:, c:c + 1], dim=0)).flatten()
+            assert torch.equal(v2[bank, :, c], var[bank, :, col[0]])
+
+
+def _coarse_by_loops(q, qsq, drift, km, vm, w, counts, part, scale, theta, nv):
+    """Independent per-row restatement of the coarse tail in float64."""
+    out = torch.zeros(q.shape[0], nv, q.shape[-1], dtype=torch.float64)
+    lse = torch.full((q.shape[0], nv), -math.inf, dtype=torch.float64)
+    for b in range(q.shape[0]):
+        for r in range(nv):
+            i = r // 128
+            logits, gated, vals = [], [], []
+            for j in range(km.shape[1]):
+                if part[b, i, j]:
+                    continue
+                quad = float(qsq[b, r].double() @ w[b, j].double())
+                gate = quad * scale * scale <= theta * theta
+                logit = (scale * float(q[b, r].double() @ km[b, j].double())
+                         + math.log(float(counts[j])) + (0.5 * scale * scale * quad if gate else 0.0))
+                logits.append(logit)
+                gated.append(gate)
+                vals.append(vm[b, j].double())
+            if not logits:
+                continue
+            lg = torch.tensor(logits, dtype=torch.float64)
+            p = torch.softmax(lg, 0)
+            gfrac = float(p[torch.tensor(gated)].sum())
+            out[b, r] = (p.unsqueeze(1) * torch.stack(vals)).sum(0) + gfrac * drift[b, r].double()
+            lse[b, r] = torch.logsumexp(lg, 0)
+    return out, lse
+
+
+def test_coarse_tail_brute_force_fp32():
+    g = torch.Generator().manual_seed(9)
+    nv, d, nb = 384, 64, 3
+    q = torch.randn(1, nv + 10, d, generator=g)
+    qsq = torch.rand(1, nv, d, generator=g) * 3
+    drift = torch.randn(1, nv, d, generator=g) * 0.1
+    km = torch.randn(1, nb, d, generator=g)
+    vm = torch.randn(1, nb, d, generator=g)
+    w = torch.rand(1, nb, d, generator=g) * torch.tensor([0.01, 1.0, 4.0]).view(1, 3, 1)
+    counts = torch.tensor([128.0, 128.0, 128.0])
+    part = torch.tensor([[[True, False, False], [False, True, False], [True, True, True]]])
+    out, lse = O.coarse_tail(q, qsq, drift, km, vm, w, counts, part, 0.125, 2.0, nv,
+                             torch.float32)
+    ref, rlse = _coarse_by_loops(q, qsq, drift, km, vm, w, counts, part, 0.125, 2.0, nv)
+    assert torch.allclose(out.double(), ref, atol=2e-5)
+    fin = torch.isfinite(rlse)
+    assert torch.equal(torch.isfinite(lse), fin) and (~fin).sum() == 128
+    assert torch.allclose(lse.double()[fin], rlse[fin], atol=2e-5)
+
+
+def test_coarse_tail_exact_for_constant_blocks():
+    # Keys constant within each block: zero variance, zero C_vk, so the coarse tail equals
+    # exact attention over the omitted tokens.
+    g = torch.Generator().manual_seed(10)
+    nv, d = 512, 64
+    kb = torch.randn(4, d, generator=g) * 0.5
+    k = kb.repeat_interleave(128, 0).unsqueeze(0)
+    v = torch.randn(1, nv, d, generator=g)
+    q = torch.randn(1, nv, d, generator=g)
+    km, counts = O.pool_blocks(k, nv)
+    vm, _ = O.pool_blocks(v, nv)
+    basis = torch.eye(d).unsqueeze(0)
+    _, var = O.rotated_moments(k, basis, counts, nv)
+    cvk = O.value_key_covariance(k, v, km, counts, nv)
+    assert var.abs().max() < 1e-10 and cvk.abs().max() < 1e-6
+    qsq = O.rotated_query_square(q, basis, torch.float32)
+    drift = O.value_drift(q, cvk, 0.125, torch.float32)
+    part = torch.eye(4, dtype=torch.bool).unsqueeze(0)
+    out, lse = O.coarse_tail(q, qsq, drift, km, vm, O.fold_rank(var, 4), counts, part, 0.125,
+                             2.0, nv, torch.float32)
+    tok = torch.arange(nv) // 128
+    s = (q[0].double() @ k[0].double().T) * 0.125
+    s = s.masked_fill(tok.view(-1, 1) == tok.view(1, -1), -math.inf)
+    ref = torch.softmax(s, -1) @ v[0].double()
+    assert torch.allclose(out[0].double(), ref, atol=1e-5)
+    assert torch.allclose(lse[0].double(), torch.logsumexp(s, -1), atol=1e-5)
+
+
+# -- stage 4 ----------------------------------------------------------------------------------
+
+
+def test_merge_with_zero_alpha_is_head_plus_coarse():
+    g = torch.Generator().manual_seed(11)
+    banks, n, d, rows = 2, 260, 64, 256
+    oh, go, det = (torch.randn(banks, m, d, generator=g) for m in (n, rows, rows))
+    lh = torch.randn(banks, n, generator=g)
+    gl = torch.randn(banks, rows, generator=g)
+    dl = torch.randn(banks, rows, generator=g)
+    out = O.sparse_merge(oh, lh, go, gl, det, dl, rows, gl, torch.zeros(banks), alpha_override=0.0)
+    wh = torch.sigmoid(lh[:, :rows] - gl).unsqueeze(-1)
+    assert torch.allclose(out[:, :rows], wh * oh[:, :rows] + (1 - wh) * go, atol=1e-5)
+    assert torch.equal(out[:, rows:], oh[:, rows:])
+    # alpha = 1 uses coarse + refinement with log-mass gl + dl
+    out1 = O.sparse_merge(oh, lh, go, gl, det, dl, rows, gl, torch.zeros(banks))
+    wh1 = torch.sigmoid(lh[:, :rows] - gl - dl).unsqueeze(-1)
+    assert torch.allclose(out1[:, :rows], wh1 * oh[:, :rows] + (1 - wh1) * (go + det), atol=1e-5)
+
+
+def test_refresh_then_sparse_reproduces_dense_cpu_config():
+    wl = WORKLOADS["cpu-plumbing"]
+    q, k, v = make_qkv(wl, seed=0)
+    op = O.OracleOperator(wl.grid, wl.text_tokens, wl.text_first, wl.density)
+    dense = op.refresh(0, q, k, v, dtype=torch.float32)
+    last = op.last
+    # dense output is exact softmax attention
+    s = (q[0, 0].double() @ k[0, 0].double().T) / 8.0
+    assert torch.allclose(dense[0, 0].double(), torch.softmax(s, -1) @ v[0, 0].double(), atol=1e-5)
+    sparse = op.sparse(0, q, k, v, dtype=torch.float32)
+    assert op.last["center"].abs().max() < 1e-6  # same inputs: no drift, alpha = 1
+    # What remains is the reference's own rounding: rows whose head holds > 99.9% of the
+    # mass get a zero refinement (error <= (1 - ratio) |exact tail - coarse|), all other rows
+    # only the fp16 rounding of D (relative 2^-11).
+    err = (sparse - dense)[0].abs()                      # [H, N, d] native
+    perm = torch.as_tensor(op.permutation, dtype=torch.long)
+    rows = last["go"].shape[1]
+    lf = last["full_l"][:, :rows]                        # reordered rows
+    of, oh, go = last["full_o"][:, :rows], last["oh"][:, :rows], last["go"]
+    ratio = torch.clamp_max(torch.exp(torch.clamp_max(last["lh"][:, :rows] - lf, 0.0)), 1 - 1e-6)
+    tail = (of - ratio.unsqueeze(-1) * oh) / (1 - ratio).unsqueeze(-1)
+    zeroed = (ratio > 1 - 1e-3).unsqueeze(-1)
+    bound = torch.where(zeroed, (1 - ratio).unsqueeze(-1) * (tail - go).abs(),
+                        op.layers[0].det.abs() * 2.0 ** -11)
+    assert (err[:, perm[:rows]] <= bound + 2e-6).all()
+    assert zeroed.any() and (~zeroed).any()
+    assert err.median() < 1e-5
+    # with the BASELINE's fixed drift weight of 0.8 the output moves toward head (+) coarse
+    partial = op.sparse(0, q, k, v, dtype=torch.float32, alpha_override=0.8)
+    assert (partial - dense).abs().max() > (sparse - dense).abs().max()
