@@ -47,7 +47,7 @@ __all__ = [
     "within_block_scatter", "closure_basis", "split_hi_lo", "rotated_moments",
     "value_key_covariance", "order_basis", "fold_rank", "rotated_query_square",
     "value_drift", "coarse_tail", "drift_center", "sparse_merge", "refresh_detail",
-    "OracleLayer", "OracleOperator", "cast",
+    "OracleLayer", "OracleOperator", "cast", "topk_margin",
 ]
 
 

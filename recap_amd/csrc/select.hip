@@ -35,7 +35,7 @@ __global__ __launch_bounds__(256) void block_scores_kernel(ScoreArgs a) {
 #pragma unroll
   for (int ai = 0; ai < 4; ++ai)
 #pragma unroll
-    for (int bj = 0; bj < 4; ++bj) acc[ai][bj] = __fmul_rn(qs[ty + 16 * ai][0], ks[tx + 16 * bj][0]);
+    for (int bj = 0; bj < 4; ++bj) acc[ai][bj] = qs[ty + 16 * ai][0] * ks[tx + 16 * bj][0];
   for (int c = 1; c < D; ++c) {
     float qv[4], kv[4];
 #pragma unroll
@@ -43,7 +43,7 @@ __global__ __launch_bounds__(256) void block_scores_kernel(ScoreArgs a) {
 #pragma unroll
     for (int ai = 0; ai < 4; ++ai)
 #pragma unroll
-      for (int bj = 0; bj < 4; ++bj) acc[ai][bj] = __fadd_rn(acc[ai][bj], __fmul_rn(qv[ai], kv[bj]));
+      for (int bj = 0; bj < 4; ++bj) acc[ai][bj] = acc[ai][bj] + qv[ai] * kv[bj];  // two roundings (contract off)
   }
   float* out = a.scores + (int64_t)bank * a.nb * a.nb;
 #pragma unroll
@@ -52,7 +52,7 @@ __global__ __launch_bounds__(256) void block_scores_kernel(ScoreArgs a) {
 #pragma unroll
     for (int bj = 0; bj < 4; ++bj) {
       const int j = j0 + tx + 16 * bj;
-      if (i < a.nb && j < a.nb) out[(int64_t)i * a.nb + j] = __fmul_rn(acc[ai][bj], a.scale);
+      if (i < a.nb && j < a.nb) out[(int64_t)i * a.nb + j] = acc[ai][bj] * a.scale;
     }
   }
 }

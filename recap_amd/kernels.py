@@ -133,6 +133,7 @@ def pool_blocks(x: torch.Tensor, rowmap: torch.Tensor, geo: Geometry) -> torch.T
 
 
 def block_scores(q_means: torch.Tensor, k_means: torch.Tensor, scale: float) -> torch.Tensor:
+    q_means, k_means = q_means.contiguous(), k_means.contiguous()
     banks, nb, d = q_means.shape
     out = torch.empty(banks, nb, nb, dtype=torch.float32, device=q_means.device)
     call("recap_block_scores", q_means.data_ptr(), k_means.data_ptr(), banks, nb, d,
@@ -226,6 +227,8 @@ class BasisTables:
 
 def basis_tables(basis: torch.Tensor | None, cvk: torch.Tensor | None, dtype: torch.dtype, *,
                  split: bool = False, query: bool = False, cvk_table: bool = False) -> BasisTables:
+    basis = None if basis is None else basis.to(torch.float32).contiguous()
+    cvk = None if cvk is None else cvk.to(torch.float32).contiguous()
     src = basis if basis is not None else cvk
     banks, d = src.shape[0], src.shape[-1]
     mk = lambda: torch.empty(banks, d, d, dtype=dtype, device=src.device)  # noqa: E731
@@ -238,6 +241,7 @@ def basis_tables(basis: torch.Tensor | None, cvk: torch.Tensor | None, dtype: to
 
 
 def coarse_tables(var: torch.Tensor, kv: PackedKV, rank: int):
+    var = var.to(torch.float32).contiguous()
     banks, nb, d = var.shape
     mk = lambda: torch.empty(banks, nb, d, dtype=kv.dtype, device=var.device)  # noqa: E731
     w, kbar, vbar = mk(), mk(), mk()
@@ -252,6 +256,8 @@ def coarse_tail(q: torch.Tensor, rowmap: torch.Tensor, partition: torch.Tensor, 
     """(go [banks, R, d], gl [banks, R], drift partial [banks, R/128] or None)."""
     b, h, n, d = q.shape
     banks = b * h
+    partition = partition.contiguous()
+    glref = None if glref is None else glref.contiguous()
     go = torch.empty(banks, geo.rows, d, dtype=q.dtype, device=q.device)
     gl = torch.empty(banks, geo.rows, dtype=torch.float32, device=q.device)
     part = None
@@ -278,6 +284,7 @@ def block_sparse_attn(q: torch.Tensor, kv: PackedKV, rowmap: torch.Tensor,
                       kernel_mask: torch.Tensor, geo: Geometry, scale: float):
     """Head branch (reordered order): (out [banks, N, d], lse [banks, N])."""
     b, h, n, d = q.shape
+    kernel_mask = kernel_mask.contiguous()
     out = torch.empty(b * h, n, d, dtype=q.dtype, device=q.device)
     lse = torch.empty(b * h, n, dtype=torch.float32, device=q.device)
     call("recap_block_sparse_attn", *_qkv_args(q), kv.k_tiles.data_ptr(), kv.vt_tiles.data_ptr(),
@@ -305,6 +312,9 @@ def sparse_merge_attn(q: torch.Tensor, kv: PackedKV, rowmap: torch.Tensor,
                       out: torch.Tensor | None = None) -> torch.Tensor:
     """Corrected sparse output [B, H, N, d] in native order (one fused kernel)."""
     b, h, n, d = q.shape
+    kernel_mask = kernel_mask.contiguous()
+    if any(t is not None and not t.is_contiguous() for t in (go, gl, det, dl, glref, center)):
+        raise ValueError("merge inputs must be contiguous")
     if out is None:
         out = torch.empty(b, h, n, d, dtype=q.dtype, device=q.device)
     alpha = -1.0 if alpha_override is None else float(alpha_override)
@@ -324,6 +334,8 @@ def refresh_capture(dense_out: torch.Tensor, dense_lse: torch.Tensor, head_out: 
                     glref: torch.Tensor | None = None, center: torch.Tensor | None = None):
     """Write the refinement in place; with (glref, center) return the validation pair."""
     b, h, n, d = dense_out.shape
+    if not all(t.is_contiguous() for t in (dense_lse, head_out, head_lse, go, gl, det, dl)):
+        raise ValueError("capture inputs must be contiguous")
     stats = part = None
     if glref is not None:
         npart = int(_lib.load().recap_capture_partials(b * h, d, geo.n_video))
