@@ -144,13 +144,13 @@ int recap_drift_center(const float* drift_partial, int64_t banks, int64_t n_vide
 /* Stage 2 ------------------------------------------------------------------------------ */
 
 /* Head branch at a refresh: exact attention over the kernel mask, reordered order:
- * head_out [banks, n_tokens, dim] (query type), head_lse [banks, n_tokens] (natural log).
+ * head_out [banks, n_tokens, dim] fp32, head_lse [banks, n_tokens] (natural log).
  * Replaces block_sparse_exact, recap/kernels/block_sparse.py:78-139. */
 int recap_block_sparse_attn(const void* q, int dtype, int64_t batch, int64_t heads,
                             int64_t dim, int64_t stride_b, int64_t stride_h, int64_t stride_n,
                             const void* k_tiles, const void* vt_tiles, const int32_t* rowmap,
                             const uint8_t* kernel_mask, int64_t n_tokens, float scale,
-                            void* head_out, float* head_lse, void* stream);
+                            float* head_out, float* head_lse, void* stream);
 
 /* Dense attention with LSE, native order: out [batch, heads, n_tokens, dim] with the
  * given strides, lse [banks, n_tokens].
@@ -182,14 +182,15 @@ int recap_sparse_merge_attn(const void* q, int dtype, int64_t batch, int64_t hea
 /* Number of (err2, ref2) partial pairs recap_refresh_capture writes. */
 int64_t recap_capture_partials(int64_t banks, int64_t dim, int64_t n_video);
 
-/* Refinement capture in place into det (fp16 [banks, R, dim]) and dl ([banks, R]).  With
+/* Refinement capture in place into det (fp16 [banks, R, dim]) and dl ([banks, R]) from the
+ * dense output (native order, query type), the fp32 head branch and the coarse tail.  With
  * glref and center non-NULL the previous refinement is scored first: stat_partial
  * receives the partial pairs and stats[2] = (sum err^2, sum ref^2).
  * Replaces refresh_detail + _refresh_detail_kernel, recap/kernels/detail_cache.py:25-186,
  * 304-379. */
 int recap_refresh_capture(const void* dense_out, int dtype, int64_t batch, int64_t heads,
                           int64_t dim, int64_t out_stride_b, int64_t out_stride_h,
-                          int64_t out_stride_n, const float* dense_lse, const void* head_out,
+                          int64_t out_stride_n, const float* dense_lse, const float* head_out,
                           const float* head_lse, const void* go, const float* gl,
                           const int32_t* rowmap, int64_t n_tokens, int64_t n_video, void* det,
                           float* dl, const float* glref, const float* center,

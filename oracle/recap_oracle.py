@@ -539,6 +539,17 @@ class OracleOperator:
     def layer(self, index: int) -> OracleLayer:
         return self.layers.setdefault(index, OracleLayer())
 
+    def load_state(self, index: int, *, basis, partition, det, dl, glref, n_tokens: int):
+        """Adopt a refinement state captured elsewhere (e.g. by the GPU operator), so a
+        sparse call can be compared on identical state.  Arrays are CPU tensors in the
+        layouts of recap/operator.py:33-59 (partition flattened to [banks, nb, nb])."""
+        state = self.layer(index)
+        state.basis = basis.float()
+        state.partition = partition.bool()
+        state.kmask = kernel_block_mask(state.partition, n_tokens, self.n_video, self.block)
+        state.det, state.dl, state.glref = det.float(), dl.float(), glref.float()
+        state.valid = True
+
     def _banks(self, x):
         b, h, n, d = x.shape
         return reorder(x, self.fwd).reshape(b * h, n, d)
@@ -587,8 +598,8 @@ class OracleOperator:
         scale = 1.0 / math.sqrt(d)
         rows = (self.n_video // self.block) * self.block
         ql, kl, vl = self._banks(q), self._banks(k), self._banks(v)
-        full_o, full_l = dense_attention(ql, kl, vl, scale, self.block)
-        full_o = cast(full_o, dtype)
+        full_o32, full_l = dense_attention(ql, kl, vl, scale, self.block)
+        full_o = cast(full_o32, dtype)
         of_native = restore(full_o, self.inv)
         lf_native = full_l.index_select(-1, self.inv)
         revalidating = state.valid
@@ -622,7 +633,8 @@ class OracleOperator:
         state.det, state.dl, state.glref = det, dl, gl.clone()
         state.valid = True
         self.last = {"ctx": ctx, "oh": oh, "lh": lh, "go": go, "gl": gl, "rerank": rerank,
-                     "full_o": full_o, "full_l": full_l}
+                     "full_o": full_o, "full_l": full_l,
+                     "out_f32": restore(full_o32, self.inv).reshape(b, h, n, d)}
         return of_native.reshape(b, h, n, d)
 
     def sparse(self, index, q, k, v, dtype=torch.bfloat16, alpha_override=None):
@@ -639,7 +651,8 @@ class OracleOperator:
         ctx = self._context(state, ql, kl, vl, dtype)
         go, gl = self._coarse(ql, ctx, state.partition, dtype, rows)
         center = drift_center(gl, state.glref)
-        merged = cast(sparse_merge(oh, lh, go, gl, state.det, state.dl, rows, state.glref,
-                                   center, alpha_override), dtype)
-        self.last = {"ctx": ctx, "oh": oh, "lh": lh, "go": go, "gl": gl, "center": center}
-        return restore(merged, self.inv).reshape(b, h, n, d)
+        merged32 = sparse_merge(oh, lh, go, gl, state.det, state.dl, rows, state.glref, center,
+                                alpha_override)
+        self.last = {"ctx": ctx, "oh": oh, "lh": lh, "go": go, "gl": gl, "center": center,
+                     "out_f32": restore(merged32, self.inv).reshape(b, h, n, d)}
+        return restore(cast(merged32, dtype), self.inv).reshape(b, h, n, d)

@@ -15,7 +15,7 @@
 // restore of recap/operator.py:496-498, 527 are fused into the loads and stores.
 //
 // Epilogues:
-//   head   (oh, lh) in reordered order -- the head branch a refresh capture needs;
+//   head   (oh fp32, lh) in reordered order -- the head branch a refresh capture needs;
 //   dense  output + LSE in native order -- a refresh's dense call;
 //   merge  head (+) [coarse tail + drift-weighted refinement] in LSE space for rows < R,
 //          the head alone above (recap/kernels/detail_cache.py:220-301), written in
@@ -170,15 +170,16 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs a) {
   const float lse = (m + log2f(lt)) * kLn2;
 
   if constexpr (MODE == kModeHead) {
-    uint16_t* orow = a.head_out + ((int64_t)bank * a.n_tokens + r) * D;
+    // fp32 head branch: the capture and the merge then see the same unrounded values.
+    float* orow = a.head_out + ((int64_t)bank * a.n_tokens + r) * D;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
         const int d0 = 32 * dt + 8 * q4 + 4 * g;
-        u32x2 v = {pack2<T>(oacc[dt][4 * q4] * inv, oacc[dt][4 * q4 + 1] * inv),
-                   pack2<T>(oacc[dt][4 * q4 + 2] * inv, oacc[dt][4 * q4 + 3] * inv)};
-        *reinterpret_cast<u32x2*>(orow + d0) = v;
+        *reinterpret_cast<f32x4*>(orow + d0) =
+            f32x4{oacc[dt][4 * q4] * inv, oacc[dt][4 * q4 + 1] * inv,
+                  oacc[dt][4 * q4 + 2] * inv, oacc[dt][4 * q4 + 3] * inv};
       }
     if (g == 0) a.head_lse[(int64_t)bank * a.n_tokens + r] = lse;
     return;
@@ -200,7 +201,8 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs a) {
   }
 
   // Merge epilogue (recap/kernels/detail_cache.py:228-301): rows < R get the drift-weighted
-  // tail; the head output enters at its stored precision.
+  // tail.  The head output is never materialised here, so it enters in fp32 (the reference
+  // rounds it to bf16 only because its attention kernel stores a bf16 tensor).
   if (r < a.rows) {
     const int64_t ri = (int64_t)bank * a.rows + r;
     const float glv = a.gl[ri], dlv = a.dl[ri];
@@ -231,7 +233,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs a) {
           const unsigned gword = gw[e >> 1], dword = dw[e >> 1];
           const float gov = T::to_f((uint16_t)((e & 1) ? gword >> 16 : gword & 0xffff));
           const float detv = f16_to_f((uint16_t)((e & 1) ? dword >> 16 : dword & 0xffff));
-          const float ohv = T::to_f(T::from_f(oacc[dt][4 * q4 + e] * inv));
+          const float ohv = oacc[dt][4 * q4 + e] * inv;
           const float to = (gov * sm + (gov + detv) * cm) / den;
           res[e] = (ohv * wh + to * wt) / den2;
         }

@@ -79,7 +79,7 @@ struct AttnArgs {
   const int32_t* rowmap; const uint8_t* kmask;   // kmask null in dense mode
   int heads, banks, n_tokens, tb, ds;
   float scale_log2;
-  uint16_t* head_out; float* head_lse;           // head mode, reordered [bank][N](D)
+  float* head_out; float* head_lse;              // head mode, reordered [bank][N](D), fp32
   uint16_t* out; int64_t osB, osH, osN;          // dense / merge, native order
   float* lse_native;                             // dense mode [bank][N]
   int rows; const uint16_t* go; const float* gl; const uint16_t* det; const float* dl;
@@ -91,7 +91,7 @@ hipError_t run_attention(const AttnArgs& a, int dtype, int dim, int mode, hipStr
 struct CaptureArgs {
   const uint16_t* of; int64_t osB, osH, osN;     // dense output, native order
   const float* lf;                               // dense LSE, native [bank][N]
-  const uint16_t* oh; const float* lh;           // head branch, reordered [bank][N](D)
+  const float* oh; const float* lh;              // head branch fp32, reordered [bank][N](D)
   const uint16_t* go; const float* gl;           // coarse branch [bank][rows](D)
   const int32_t* rowmap;
   int heads, banks, n_tokens, rows;

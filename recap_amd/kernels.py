@@ -282,10 +282,10 @@ def drift_center(part: torch.Tensor, geo: Geometry) -> torch.Tensor:
 
 def block_sparse_attn(q: torch.Tensor, kv: PackedKV, rowmap: torch.Tensor,
                       kernel_mask: torch.Tensor, geo: Geometry, scale: float):
-    """Head branch (reordered order): (out [banks, N, d], lse [banks, N])."""
+    """Head branch (reordered order): (out [banks, N, d] fp32, lse [banks, N])."""
     b, h, n, d = q.shape
     kernel_mask = kernel_mask.contiguous()
-    out = torch.empty(b * h, n, d, dtype=q.dtype, device=q.device)
+    out = torch.empty(b * h, n, d, dtype=torch.float32, device=q.device)
     lse = torch.empty(b * h, n, dtype=torch.float32, device=q.device)
     call("recap_block_sparse_attn", *_qkv_args(q), kv.k_tiles.data_ptr(), kv.vt_tiles.data_ptr(),
          rowmap.data_ptr(), kernel_mask.data_ptr(), n, float(scale), out.data_ptr(),

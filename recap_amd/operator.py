@@ -389,6 +389,12 @@ class Operator:
 
     # -- sparse --------------------------------------------------------------------------
 
+    def _mark(self, name: str) -> None:
+        if self.stage_events is not None:
+            event = torch.cuda.Event(enable_timing=True)
+            event.record()
+            self.stage_events.setdefault(name, []).append(event)
+
     @torch.no_grad()
     def _sparse(self, layer, bank, q, k, v, geo, rowmap, out=None) -> torch.Tensor:
         """Head exactly, plus coarse tail and weighted cached refinement

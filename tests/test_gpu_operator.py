@@ -27,41 +27,82 @@ def build(wl, *, chunks=1, host_banks=False, prefetch=True, layers=2):
     return op, perm
 
 
+def inject(ref, op, layer_index, wl):
+    """Give the oracle the GPU operator's refinement state (basis, partition, D, DL, gl_ref)."""
+    bank, layer = op.banks[0][layer_index], op.layers[0][layer_index]
+    nb = bank.partition.shape[-1]
+    ref.load_state(layer_index, basis=layer.basis.cpu(),
+                   partition=bank.partition.reshape(-1, nb, nb).cpu(),
+                   det=bank.value.cpu(), dl=bank.log_mass.cpu(), glref=bank.coarse_lse.cpu(),
+                   n_tokens=wl.tokens)
+
+
 @pytest.mark.parametrize("name", list(SMALL))
 def test_refresh_sparse_sequence_vs_oracle(cuda, name):
+    """REFRESH / SPARSE / REFRESH (revalidation) / SPARSE against the oracle operator.
+
+    Each sparse call is compared on the same refinement state (the GPU's state is handed to
+    the oracle after every refresh) with the oracle's unrounded fp32 output as reference:
+    the hot path must then agree within max-abs 2e-2 and cosine 0.999."""
     wl = SMALL[name]
     print(f"case {name}", flush=True)
     q, k, v = make_qkv(wl, seed=0)
     op, perm = build(wl)
     ref = O.OracleOperator(wl.grid, wl.text_tokens, wl.text_first, wl.density, permutation=perm)
     g = lambda x: x.to(cuda)  # noqa: E731
-    # step 0: first refresh (selection, basis, capture)
     op.begin_step(0, REFRESH)
     out = op.attend(0, g(q), g(k), g(v))
-    dense_ref = ref.refresh(0, q, k, v)
-    assert_close_bf16(out.cpu().float(), dense_ref, f"refresh-0 {name}")
+    ref.refresh(0, q, k, v)
+    assert_close_bf16(out.cpu().float(), ref.last["out_f32"], f"refresh-0 {name}")
     bank = op.banks[0][0]
     assert torch.equal(bank.partition.cpu().reshape(ref.layers[0].partition.shape),
                        ref.layers[0].partition)
-    # step 1: sparse call on drifted inputs
+    inject(ref, op, 0, wl)
     q1, k1, v1 = (perturb(x, 0.02, seed=1, step=1) for x in (q, k, v))
     op.begin_step(1, SPARSE)
     out = op.attend(0, g(q1), g(k1), g(v1))
-    assert_close_bf16(out.cpu().float(), ref.sparse(0, q1, k1, v1), f"sparse-1 {name}")
-    # step 2: refresh with revalidation of the old refinement
+    ref.sparse(0, q1, k1, v1)
+    assert_close_bf16(out.cpu().float(), ref.last["out_f32"], f"sparse-1 {name}")
     q2, k2, v2 = (perturb(x, 0.03, seed=1, step=2) for x in (q, k, v))
     op.begin_step(2, REFRESH)
     out = op.attend(0, g(q2), g(k2), g(v2))
-    assert_close_bf16(out.cpu().float(), ref.refresh(0, q2, k2, v2), f"refresh-2 {name}")
+    ref.refresh(0, q2, k2, v2)
+    assert_close_bf16(out.cpu().float(), ref.last["out_f32"], f"refresh-2 {name}")
     age, error = op.drain_validation()
     num, den = (float(x) for x in ref.layers[0].pending_stats)
-    print(f"  validation error gpu={error:.5f} oracle={math.sqrt(num / den):.5f}", flush=True)
+    print(f"  validation error gpu={error:.5f} oracle={math.sqrt(num / den):.5f} "
+          f"rerank={ref.last['rerank']}", flush=True)
     assert age == 2 and abs(error - math.sqrt(num / den)) < 2e-3
-    # step 3: sparse again
+    inject(ref, op, 0, wl)
     q3, k3, v3 = (perturb(x, 0.02, seed=1, step=3) for x in (q, k, v))
     op.begin_step(3, SPARSE)
     out = op.attend(0, g(q3), g(k3), g(v3))
-    assert_close_bf16(out.cpu().float(), ref.sparse(0, q3, k3, v3), f"sparse-3 {name}")
+    ref.sparse(0, q3, k3, v3)
+    assert_close_bf16(out.cpu().float(), ref.last["out_f32"], f"sparse-3 {name}")
+
+
+@pytest.mark.parametrize("name", list(SMALL))
+def test_sparse_vs_oracle_with_independent_state(cuda, name):
+    """End to end with separately computed refinement states.  The coarse tail's gate
+    [s^2 qsq.w <= theta^2] is discontinuous and D = (of - ratio oh)/(1 - ratio) - go
+    amplifies last-bit differences of the bf16 dense/head outputs, so a few elements may
+    move by more than a bf16 ulp; the bulk must still agree."""
+    wl = SMALL[name]
+    q, k, v = make_qkv(wl, seed=0)
+    op, perm = build(wl)
+    ref = O.OracleOperator(wl.grid, wl.text_tokens, wl.text_first, wl.density, permutation=perm)
+    op.begin_step(0, REFRESH)
+    op.attend(0, q.to(cuda), k.to(cuda), v.to(cuda))
+    ref.refresh(0, q, k, v)
+    q1, k1, v1 = (perturb(x, 0.02, seed=1, step=1) for x in (q, k, v))
+    op.begin_step(1, SPARSE)
+    out = op.attend(0, q1.to(cuda), k1.to(cuda), v1.to(cuda)).cpu().float()
+    ref.sparse(0, q1, k1, v1)
+    want = ref.last["out_f32"]
+    m, c = metrics(out, want)
+    frac = float(((out - want).abs() > 2e-2).float().mean())
+    print(f"[independent {name}] max_abs={m:.3e} cos={c:.6f} frac>2e-2={frac:.2e}", flush=True)
+    assert c >= 0.999 and frac <= 1e-3 and m < 0.25
 
 
 def test_alpha_override_knob_vs_oracle(cuda):
@@ -71,13 +112,13 @@ def test_alpha_override_knob_vs_oracle(cuda):
     ref = O.OracleOperator(wl.grid, wl.text_tokens, wl.text_first, wl.density, permutation=perm)
     op.begin_step(0, REFRESH)
     op.attend(0, q.to(cuda), k.to(cuda), v.to(cuda))
-    ref.refresh(0, q, k, v)
+    inject(ref, op, 0, wl)
     q1, k1, v1 = (perturb(x, 0.05, seed=2, step=1) for x in (q, k, v))
     op.alpha_override = 0.8
     op.begin_step(1, SPARSE)
     out = op.attend(0, q1.to(cuda), k1.to(cuda), v1.to(cuda))
-    assert_close_bf16(out.cpu().float(), ref.sparse(0, q1, k1, v1, alpha_override=0.8),
-                      "alpha=0.8")
+    ref.sparse(0, q1, k1, v1, alpha_override=0.8)
+    assert_close_bf16(out.cpu().float(), ref.last["out_f32"], "alpha=0.8")
 
 
 def test_sparse_before_refresh_raises(cuda):
