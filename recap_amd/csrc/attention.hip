@@ -20,24 +20,35 @@
 //   merge  head (+) [coarse tail + drift-weighted refinement] in LSE space for rows < R,
 //          the head alone above (recap/kernels/detail_cache.py:220-301), written in
 //          native order: the whole corrected sparse output in one pass.
+#include <type_traits>
+
 #include "kernels.hpp"
 
 namespace recap {
 
 constexpr int kMaxTiles = 2048;
 
+// Rows whose running max grows by less than this (log2 units) keep their stale max: p then
+// stays below 2^8, exact in fp32 and bf16, and the O rescale is skipped.
+constexpr float kRescaleSlack = 8.0f;
+
 template <class T, int D, int MODE>
 __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs a) {
   using G = TileGeom<D>;
-  constexpr int NS = D / 16;   // k-steps over the head dimension
-  constexpr int NDT = D / 32;  // 32-row tiles of O^T
-  __shared__ __attribute__((aligned(16))) char k_lds[G::kTileBytes];
-  __shared__ __attribute__((aligned(16))) char v_lds[G::kTileBytes];
+  constexpr int NS = D / 16;                  // k-steps over the head dimension
+  constexpr int NDT = D / 32;                 // 32-row tiles of O^T
+  constexpr int HALF = G::kHalfBytes;         // K or V^T part of a 64-key sub-tile
+  constexpr int SUB = 2 * HALF;               // one sub-tile image in LDS
+  constexpr int NLD = SUB / 16 / 256;         // 16-byte loads per thread per sub-tile
+  __shared__ __attribute__((aligned(16))) char lds[2 * SUB];
   __shared__ int list[MODE == kModeDense ? 1 : kMaxTiles];
   __shared__ int scan[256];
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, g = lane >> 5, l32 = lane & 31;
-  const int lin = xcd_linear(blockIdx.x, a.banks * a.tb);
+  // Bank-major order across all XCDs (workgroup i runs on XCD i % 8): the workgroups in
+  // flight cover one or two banks, whose K/V tiles (61 MB per bank at the HunyuanVideo
+  // shape) then stay resident in the 256 MB Infinity Cache.
+  const int lin = blockIdx.x;
   const int bank = lin / a.tb;
   const int k_in_bank = lin % a.tb;
   const int ndense = a.tb - a.ds;  // dense query blocks first: they are the longest
@@ -65,10 +76,35 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs a) {
     nkeep = scan[255];
     __syncthreads();
   }
+  const int nsub = 2 * nkeep;  // 64-key sub-tiles
+
+  // Sub-tile `it` = half (it & 1) of kept tile (it >> 1): its K rows and its V^T half are
+  // each HALF contiguous bytes of the packed images.
+  u32x4 pre[NLD];
+  auto fetch = [&](int it) {
+    const int j = MODE == kModeDense ? (it >> 1) : list[it >> 1];
+    const int64_t tile = ((int64_t)bank * a.tb + j) * G::kTileElems;
+    const u32x4* ks = reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(a.kp + tile) + (it & 1) * HALF);
+    const u32x4* vs = reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(a.vp + tile) + (it & 1) * HALF);
+#pragma unroll
+    for (int i = 0; i < NLD / 2; ++i) {
+      pre[i] = ks[t + 256 * i];
+      pre[NLD / 2 + i] = vs[t + 256 * i];
+    }
+  };
+  auto stash = [&](int buf) {
+    u32x4* dst = reinterpret_cast<u32x4*>(lds + buf * SUB);
+#pragma unroll
+    for (int i = 0; i < NLD / 2; ++i) {
+      dst[t + 256 * i] = pre[i];
+      dst[HALF / 16 + t + 256 * i] = pre[NLD / 2 + i];
+    }
+  };
 
   const int r = qt * kBlock + wave * 32 + l32;
   const bool rv = r < a.n_tokens;
   const int nat = rv ? a.rowmap[r] : 0;
+  if (nsub > 0) fetch(0);
   u32x4 qreg[NS];
   {
     const uint16_t* qrow = a.q + b * a.qsB + h * a.qsH + (int64_t)nat * a.qsN;
@@ -77,6 +113,9 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs a) {
       qreg[s] = rv ? *reinterpret_cast<const u32x4*>(qrow + 16 * s + 8 * g) : u32x4{0u, 0u, 0u, 0u};
     }
   }
+  if (nsub > 0) stash(0);
+  if (nsub > 1) fetch(1);
+  __syncthreads();
 
   float m = -INFINITY, lsum = 0.0f;
   f32x16 oacc[NDT];
@@ -84,29 +123,14 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs a) {
   for (int dt = 0; dt < NDT; ++dt) oacc[dt] = f32x16{};
   const bool ragged = (a.n_tokens % kBlock) != 0;
 
-  for (int it = 0; it < nkeep; ++it) {
-    const int j = MODE == kModeDense ? it : list[it];
-    __syncthreads();
-    {
-      const u32x4* ks = reinterpret_cast<const u32x4*>(a.kp + ((int64_t)bank * a.tb + j) * G::kTileElems);
-      const u32x4* vs = reinterpret_cast<const u32x4*>(a.vp + ((int64_t)bank * a.tb + j) * G::kTileElems);
-      u32x4 kv[G::kTileBytes / 16 / 256], vv[G::kTileBytes / 16 / 256];
-#pragma unroll
-      for (int i = 0; i < G::kTileBytes / 16 / 256; ++i) {
-        kv[i] = ks[t + 256 * i];
-        vv[i] = vs[t + 256 * i];
-      }
-#pragma unroll
-      for (int i = 0; i < G::kTileBytes / 16 / 256; ++i) {
-        reinterpret_cast<u32x4*>(k_lds)[t + 256 * i] = kv[i];
-        reinterpret_cast<u32x4*>(v_lds)[t + 256 * i] = vv[i];
-      }
-    }
-    __syncthreads();
+  auto step = [&](int it, auto ragged_tag) {
+    constexpr bool kRagged = decltype(ragged_tag)::value;
+    const char* k_lds = lds + (it & 1) * SUB;
+    const char* v_lds = k_lds + HALF;
 
-    f32x16 sacc[4];
+    f32x16 sacc[2];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
+    for (int kt = 0; kt < 2; ++kt) {
       sacc[kt] = f32x16{};
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
@@ -114,37 +138,41 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs a) {
         sacc[kt] = T::mfma32(ka, qreg[s], sacc[kt]);
       }
     }
-    if (ragged && j == a.tb - 1) {
+    if constexpr (kRagged) {
+      const int limit = a.n_tokens - ((a.tb - 1) * kBlock + 64 * (it & 1));
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+      for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int rr = 0; rr < 16; ++rr)
-          if (j * kBlock + 32 * kt + mfma_row(rr, g) >= a.n_tokens) sacc[kt][rr] = -INFINITY;
+          if (32 * kt + mfma_row(rr, g) >= limit) sacc[kt][rr] = -INFINITY;
     }
 
     float mx = -INFINITY;
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int rr = 0; rr < 16; ++rr) mx = fmaxf(mx, sacc[kt][rr]);
-    mx = pair_max(mx);
-    const float mnew = fmaxf(m, mx * a.scale_log2);
-    const float alpha = exp2f(m - mnew);
-    lsum *= alpha;
+    const float mt = pair_max(mx) * a.scale_log2;
+    const bool grow = mt > m + kRescaleSlack;
+    if (__any(grow)) {
+      const float mnew = grow ? mt : m;
+      const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+      lsum *= alpha;
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) oacc[dt] *= alpha;
-    m = mnew;
+      for (int dt = 0; dt < NDT; ++dt) oacc[dt] *= alpha;
+      m = mnew;
+    }
 
-    u32x4 pk[4][2];
+    u32x4 pk[2][2];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
+    for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         unsigned w[4];
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
-          const float p0 = exp2f(fmaf(sacc[kt][8 * hh + e], a.scale_log2, -mnew));
-          const float p1 = exp2f(fmaf(sacc[kt][8 * hh + e + 1], a.scale_log2, -mnew));
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(sacc[kt][8 * hh + e], a.scale_log2, -m));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(sacc[kt][8 * hh + e + 1], a.scale_log2, -m));
           lsum += p0 + p1;
           w[e >> 1] = pack2<T>(p0, p1);
         }
@@ -154,7 +182,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs a) {
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
+      for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
           const u32x4 va = lds_load16(v_lds, G::vt_off(32 * dt + l32, 4 * kt + 2 * hh + g));
@@ -162,7 +190,19 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs a) {
         }
       }
     }
-  }
+
+    // Sub-tile it+1 (fetched during this one) goes to the other buffer, whose last reader
+    // was iteration it-1; then fetch it+2 and wait for everyone.
+    if (it + 1 < nsub) stash((it + 1) & 1);
+    if (it + 2 < nsub) fetch(it + 2);
+    __syncthreads();
+  };
+  // The last kept tile holds the ragged keys when it is the sequence's last block.
+  const bool ragged_last = ragged && nkeep > 0 &&
+                           (MODE == kModeDense ? true : list[nkeep - 1] == a.tb - 1);
+  const int plain = ragged_last ? nsub - 2 : nsub;
+  for (int it = 0; it < plain; ++it) step(it, std::false_type{});
+  for (int it = plain; it < nsub; ++it) step(it, std::true_type{});
 
   if (!rv) return;
   const float lt = pair_sum(lsum);

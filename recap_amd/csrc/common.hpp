@@ -52,9 +52,19 @@ __device__ inline uint16_t f_to_bf16(float f) { return BF16::from_f(f); }
 __device__ inline float f16_to_f(uint16_t h) { return F16::to_f(h); }
 __device__ inline uint16_t f_to_f16(float f) { return F16::from_f(f); }
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Two fp32 values rounded to the 16-bit type and packed (lo in bits 0-15): one
+// v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32 per pair.
 template <class T>
 __device__ inline unsigned pack2(float lo, float hi) {
-  return (unsigned)T::from_f(lo) | ((unsigned)T::from_f(hi) << 16);
+  if constexpr (T::code == 2) {
+    return __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
+  } else {
+    return __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2{lo, hi}, f16x2));
+  }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -105,20 +115,31 @@ __device__ inline int xcd_linear(int bid, int n) {
   return xcd * per + min(xcd, rem) + slot;
 }
 
-// Packed tile geometry: a K tile is [128 keys][D] with its 16-byte chunks XOR-swizzled
-// by key row; a V^T tile is [D][128 positions] where position p holds key swap23(p),
-// chunks swizzled by the d row.  The images are copied verbatim into LDS.
+// Packed tile geometry.  A K tile is [128 keys][D] with its 16-byte chunks XOR-swizzled by
+// key row.  A V^T tile is two halves (keys 0-63, 64-127), each [D][64 positions] with
+// 128-byte rows whose chunks are swizzled by d row; position p of the tile holds key
+// swap23(p).  Keys 64h.. of K and half h of V^T are each one contiguous block, so a 64-key
+// sub-tile is two contiguous images the attention kernel copies verbatim into LDS.
 template <int D>
 struct TileGeom {
   static constexpr int kRowBytes = D * 2;           // K tile row
   static constexpr int kChunks = D / 8;             // 16-byte chunks per K row
   static constexpr int kTileElems = kBlock * D;     // elements per K (or V^T) tile
   static constexpr int kTileBytes = kTileElems * 2;
+  static constexpr int kHalfBytes = kTileBytes / 2; // one 64-key half of K or of V^T
   __host__ __device__ static inline int k_off(int key, int chunk) {  // bytes
-    return key * kRowBytes + ((chunk ^ (key & (kChunks - 1))) << 4);
+    return key * kRowBytes + ((chunk ^ swz(key, kChunks)) << 4);
   }
-  __host__ __device__ static inline int vt_off(int d, int chunk) {  // bytes, 16 chunks/row
-    return d * 256 + ((chunk ^ (d & 15)) << 4);
+  // chunk c (0..15) of V^T row d: positions 8c..8c+7
+  __host__ __device__ static inline int vt_off(int d, int c) {  // bytes
+    return (c >> 3) * kHalfBytes + d * 128 + (((c & 7) ^ swz(d, 8)) << 4);
+  }
+  // XOR pattern for rows of `chunks` 16-byte chunks: any 16 consecutive rows read at one
+  // logical chunk land on distinct banks whether LDS serves 8 lanes x 16 B over 32 banks or
+  // 16 lanes over 64 banks per cycle.  With 8-chunk (128-byte) rows, rows r and r+8 share
+  // the bank half of r's parity, so bit 3 of the row flips the lowest chunk bit.
+  __host__ __device__ static inline int swz(int row, int chunks) {
+    return chunks == 16 ? (row & 15) : ((row & 7) ^ ((row >> 3) & 1));
   }
 };
 

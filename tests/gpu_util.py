@@ -60,25 +60,32 @@ def assert_close_bf16(got, ref, what, max_abs=2e-2, cos=0.999):
     assert excess <= 0 and c >= cos, f"{what}: max_abs={m} cos={c} excess={excess}"
 
 
+def swz(row: int, chunks: int) -> int:
+    """XOR pattern of the packed tile images (csrc/common.hpp TileGeom::swz)."""
+    return (row & 15) if chunks == 16 else ((row & 7) ^ ((row >> 3) & 1))
+
+
 def k_tile_to_rows(tile: torch.Tensor, d: int) -> torch.Tensor:
-    """Undo the K tile image (chunk c of key row k at chunk c ^ (k % (d/8)))."""
+    """Undo the K tile image (chunk c of key row k stored at chunk c ^ swz(k))."""
     nch = d // 8
     img = tile.reshape(BLOCK, nch, 8)
     out = torch.empty_like(img)
     for key in range(BLOCK):
         for c in range(nch):
-            out[key, c] = img[key, c ^ (key % nch)]
+            out[key, c] = img[key, c ^ swz(key, nch)]
     return out.reshape(BLOCK, d)
 
 
 def vt_tile_to_rows(tile: torch.Tensor, d: int) -> torch.Tensor:
-    """Undo the V^T tile image: row d, chunk c at c ^ (d % 16); position p holds key
-    swap23(p).  Returns V rows [128, d]."""
-    img = tile.reshape(d, 16, 8)
+    """Undo the V^T tile image: half h (positions 64h..64h+63) is [d][64] with 128-byte rows,
+    chunk c of row r stored at chunk c ^ swz(r, 8); position p holds key swap23(p).
+    Returns V rows [128, d]."""
+    halves = tile.reshape(2, d, 8, 8)
     vt = torch.empty(d, BLOCK, dtype=tile.dtype)
-    for row in range(d):
-        for c in range(16):
-            vt[row, 8 * c:8 * c + 8] = img[row, c ^ (row % 16)]
+    for h in range(2):
+        for row in range(d):
+            for c in range(8):
+                vt[row, 64 * h + 8 * c:64 * h + 8 * c + 8] = halves[h, row, c ^ swz(row, 8)]
     keys = [(p & ~12) | ((p & 4) << 1) | ((p & 8) >> 1) for p in range(BLOCK)]
     out = torch.empty(BLOCK, d, dtype=tile.dtype)
     out[keys] = vt.T

@@ -7,7 +7,7 @@ import pytest
 import torch
 
 import oracle as O
-from gpu_util import SMALL, assert_close_bf16, metrics
+from gpu_util import SMALL, assert_close_bf16, bf16_ulp, metrics
 from recap_amd import HostBankOperator, Operator, OperatorConfig, REFRESH, SPARSE
 from recap_amd.layout import Layout, SparseGeometry, hilbert_permutation
 from recap_amd.synthetic import WORKLOADS, make_qkv, perturb
@@ -100,8 +100,10 @@ def test_sparse_vs_oracle_with_independent_state(cuda, name):
     ref.sparse(0, q1, k1, v1)
     want = ref.last["out_f32"]
     m, c = metrics(out, want)
-    frac = float(((out - want).abs() > 2e-2).float().mean())
-    print(f"[independent {name}] max_abs={m:.3e} cos={c:.6f} frac>2e-2={frac:.2e}", flush=True)
+    tol = torch.clamp_min(1.5 * bf16_ulp(want), 2e-2)
+    frac = float(((out - want).abs() > tol).float().mean())
+    print(f"[independent {name}] max_abs={m:.3e} cos={c:.6f} frac-beyond-tolerance={frac:.2e}",
+          flush=True)
     assert c >= 0.999 and frac <= 1e-3 and m < 0.25
 
 
