@@ -32,180 +32,38 @@ constexpr int kMaxTiles = 2048;
 // stays below 2^8, exact in fp32 and bf16, and the O rescale is skipped.
 constexpr float kRescaleSlack = 8.0f;
 
+typedef __attribute__((address_space(3))) void lds_void;
+
+// s_waitcnt immediate (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
+// that waits for all vector memory operations of this wave -- the tile copies into LDS --
+// and all its LDS reads.
+constexpr int kWaitVmLgkm0 = 0x7 << 4;
+
+// Word 3 of a raw buffer resource on CDNA (32-bit data format, no swizzle).
+constexpr int kBufferRsrcWord3 = 0x00020000;
+
+// Wait for this wave's copies into LDS and its LDS reads, then for every wave of the
+// workgroup: afterwards the copied sub-tiles are visible and the slots read so far may be
+// overwritten.  The copies count on vmcnt only, so the wait is spelled out.
+__device__ inline void tile_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(kWaitVmLgkm0);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Each wave owns kGroups groups of 32 query rows, so every K/V fragment it reads from LDS
+// feeds kGroups MFMAs; a 128-row query block then takes kThreads threads.
+constexpr int kGroups = 1;
+constexpr int kRowsPerWave = 32 * kGroups;
+constexpr int kThreads = 64 * (kBlock / kRowsPerWave);
+
+// Final normalisation and store of one query row per lane pair (lane l holds output columns
+// 32 dt + 8 q4 + 4 g .. +3 of the row), in the layout of the kernel's mode.
 template <class T, int D, int MODE>
-__global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs a) {
-  using G = TileGeom<D>;
-  constexpr int NS = D / 16;                  // k-steps over the head dimension
-  constexpr int NDT = D / 32;                 // 32-row tiles of O^T
-  constexpr int HALF = G::kHalfBytes;         // K or V^T part of a 64-key sub-tile
-  constexpr int SUB = 2 * HALF;               // one sub-tile image in LDS
-  constexpr int NLD = SUB / 16 / 256;         // 16-byte loads per thread per sub-tile
-  __shared__ __attribute__((aligned(16))) char lds[2 * SUB];
-  __shared__ int list[MODE == kModeDense ? 1 : kMaxTiles];
-  __shared__ int scan[256];
-
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, g = lane >> 5, l32 = lane & 31;
-  // Bank-major order across all XCDs (workgroup i runs on XCD i % 8): the workgroups in
-  // flight cover one or two banks, whose K/V tiles (61 MB per bank at the HunyuanVideo
-  // shape) then stay resident in the 256 MB Infinity Cache.
-  const int lin = blockIdx.x;
-  const int bank = lin / a.tb;
-  const int k_in_bank = lin % a.tb;
-  const int ndense = a.tb - a.ds;  // dense query blocks first: they are the longest
-  const int qt = k_in_bank < ndense ? a.ds + k_in_bank : k_in_bank - ndense;
-  const int b = bank / a.heads, h = bank % a.heads;
-
-  int nkeep = a.tb;
-  if constexpr (MODE != kModeDense) {
-    const uint8_t* mrow = a.kmask + ((int64_t)bank * a.tb + qt) * a.tb;
-    const int per = (a.tb + 255) / 256;
-    const int j0 = min(t * per, a.tb), j1 = min(j0 + per, a.tb);
-    int cnt = 0;
-    for (int j = j0; j < j1; ++j) cnt += mrow[j] != 0;
-    scan[t] = cnt;
-    __syncthreads();
-    for (int off = 1; off < 256; off <<= 1) {
-      const int v = t >= off ? scan[t - off] : 0;
-      __syncthreads();
-      scan[t] += v;
-      __syncthreads();
-    }
-    int pos = scan[t] - cnt;
-    for (int j = j0; j < j1; ++j)
-      if (mrow[j]) list[pos++] = j;
-    nkeep = scan[255];
-    __syncthreads();
-  }
-  const int nsub = 2 * nkeep;  // 64-key sub-tiles
-
-  // Sub-tile `it` = half (it & 1) of kept tile (it >> 1): its K rows and its V^T half are
-  // each HALF contiguous bytes of the packed images.
-  u32x4 pre[NLD];
-  auto fetch = [&](int it) {
-    const int j = MODE == kModeDense ? (it >> 1) : list[it >> 1];
-    const int64_t tile = ((int64_t)bank * a.tb + j) * G::kTileElems;
-    const u32x4* ks = reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(a.kp + tile) + (it & 1) * HALF);
-    const u32x4* vs = reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(a.vp + tile) + (it & 1) * HALF);
-#pragma unroll
-    for (int i = 0; i < NLD / 2; ++i) {
-      pre[i] = ks[t + 256 * i];
-      pre[NLD / 2 + i] = vs[t + 256 * i];
-    }
-  };
-  auto stash = [&](int buf) {
-    u32x4* dst = reinterpret_cast<u32x4*>(lds + buf * SUB);
-#pragma unroll
-    for (int i = 0; i < NLD / 2; ++i) {
-      dst[t + 256 * i] = pre[i];
-      dst[HALF / 16 + t + 256 * i] = pre[NLD / 2 + i];
-    }
-  };
-
-  const int r = qt * kBlock + wave * 32 + l32;
-  const bool rv = r < a.n_tokens;
-  const int nat = rv ? a.rowmap[r] : 0;
-  if (nsub > 0) fetch(0);
-  u32x4 qreg[NS];
-  {
-    const uint16_t* qrow = a.q + b * a.qsB + h * a.qsH + (int64_t)nat * a.qsN;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      qreg[s] = rv ? *reinterpret_cast<const u32x4*>(qrow + 16 * s + 8 * g) : u32x4{0u, 0u, 0u, 0u};
-    }
-  }
-  if (nsub > 0) stash(0);
-  if (nsub > 1) fetch(1);
-  __syncthreads();
-
-  float m = -INFINITY, lsum = 0.0f;
-  f32x16 oacc[NDT];
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) oacc[dt] = f32x16{};
-  const bool ragged = (a.n_tokens % kBlock) != 0;
-
-  auto step = [&](int it, auto ragged_tag) {
-    constexpr bool kRagged = decltype(ragged_tag)::value;
-    const char* k_lds = lds + (it & 1) * SUB;
-    const char* v_lds = k_lds + HALF;
-
-    f32x16 sacc[2];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      sacc[kt] = f32x16{};
-#pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        const u32x4 ka = lds_load16(k_lds, G::k_off(32 * kt + l32, 2 * s + g));
-        sacc[kt] = T::mfma32(ka, qreg[s], sacc[kt]);
-      }
-    }
-    if constexpr (kRagged) {
-      const int limit = a.n_tokens - ((a.tb - 1) * kBlock + 64 * (it & 1));
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int rr = 0; rr < 16; ++rr)
-          if (32 * kt + mfma_row(rr, g) >= limit) sacc[kt][rr] = -INFINITY;
-    }
-
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int rr = 0; rr < 16; ++rr) mx = fmaxf(mx, sacc[kt][rr]);
-    const float mt = pair_max(mx) * a.scale_log2;
-    const bool grow = mt > m + kRescaleSlack;
-    if (__any(grow)) {
-      const float mnew = grow ? mt : m;
-      const float alpha = __builtin_amdgcn_exp2f(m - mnew);
-      lsum *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) oacc[dt] *= alpha;
-      m = mnew;
-    }
-
-    u32x4 pk[2][2];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        unsigned w[4];
-#pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-          const float p0 = __builtin_amdgcn_exp2f(fmaf(sacc[kt][8 * hh + e], a.scale_log2, -m));
-          const float p1 = __builtin_amdgcn_exp2f(fmaf(sacc[kt][8 * hh + e + 1], a.scale_log2, -m));
-          lsum += p0 + p1;
-          w[e >> 1] = pack2<T>(p0, p1);
-        }
-        pk[kt][hh] = u32x4{w[0], w[1], w[2], w[3]};
-      }
-    }
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          const u32x4 va = lds_load16(v_lds, G::vt_off(32 * dt + l32, 4 * kt + 2 * hh + g));
-          oacc[dt] = T::mfma32(va, pk[kt][hh], oacc[dt]);
-        }
-      }
-    }
-
-    // Sub-tile it+1 (fetched during this one) goes to the other buffer, whose last reader
-    // was iteration it-1; then fetch it+2 and wait for everyone.
-    if (it + 1 < nsub) stash((it + 1) & 1);
-    if (it + 2 < nsub) fetch(it + 2);
-    __syncthreads();
-  };
-  // The last kept tile holds the ragged keys when it is the sequence's last block.
-  const bool ragged_last = ragged && nkeep > 0 &&
-                           (MODE == kModeDense ? true : list[nkeep - 1] == a.tb - 1);
-  const int plain = ragged_last ? nsub - 2 : nsub;
-  for (int it = 0; it < plain; ++it) step(it, std::false_type{});
-  for (int it = plain; it < nsub; ++it) step(it, std::true_type{});
-
-  if (!rv) return;
-  const float lt = pair_sum(lsum);
+__device__ inline void store_rows(const AttnArgs& a, int bank, int b, int h, int r, int nat,
+                                  int g, const f32x16 (&oacc)[D / 32], float m, float lt) {
+  constexpr int NDT = D / 32;
   const float inv = 1.0f / lt;
   const float lse = (m + log2f(lt)) * kLn2;
 
@@ -293,9 +151,295 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs a) {
   }
 }
 
+
+template <class T, int D, int MODE>
+__global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
+  using G = TileGeom<D>;
+  constexpr int NS = D / 16;                  // k-steps over the head dimension
+  constexpr int NDT = D / 32;                 // 32-row tiles of O^T
+  constexpr int HALF = G::kHalfBytes;         // K or V^T image of a 64-key sub-tile
+  constexpr int NDMA = HALF / (16 * kThreads);  // 16-byte copies per thread per image
+  // LDS: K images of sub-tiles 2k / 2k+1 in slots 0 / 1, V^T images likewise after them.
+  __shared__ __attribute__((aligned(16))) char lds[4 * HALF];
+  __shared__ int list[MODE == kModeDense ? 1 : kMaxTiles];
+  __shared__ int scan[kThreads];
+
+  const int t = threadIdx.x, lane = t & 63, g = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  // Runs of 64 query blocks per XCD (about the workgroups one XCD holds at once): the
+  // neighbouring Hilbert-ordered blocks in flight on an XCD share many key tiles in its L2,
+  // and all XCDs together stay within ~512 blocks of one bank, whose K/V images (58 MB at
+  // the HunyuanVideo shape) stay in the 256 MB Infinity Cache.
+  const int lin = xcd_runs(blockIdx.x, gridDim.x, 64);
+  const int bank = lin / a.tb;
+  const int k_in_bank = lin % a.tb;
+  const int ndense = a.tb - a.ds;  // dense query blocks first: they are the longest
+  const int qt = k_in_bank < ndense ? a.ds + k_in_bank : k_in_bank - ndense;
+  const int b = bank / a.heads, h = bank % a.heads;
+
+  int nkeep = a.tb;
+  if constexpr (MODE != kModeDense) {
+    const uint8_t* mrow = a.kmask + ((int64_t)bank * a.tb + qt) * a.tb;
+    const int per = (a.tb + kThreads - 1) / kThreads;
+    const int j0 = min(t * per, a.tb), j1 = min(j0 + per, a.tb);
+    int cnt = 0;
+    for (int j = j0; j < j1; ++j) cnt += mrow[j] != 0;
+    scan[t] = cnt;
+    __syncthreads();
+    for (int off = 1; off < kThreads; off <<= 1) {
+      const int v = t >= off ? scan[t - off] : 0;
+      __syncthreads();
+      scan[t] += v;
+      __syncthreads();
+    }
+    int pos = scan[t] - cnt;
+    for (int j = j0; j < j1; ++j)
+      if (mrow[j]) list[pos++] = j;
+    nkeep = scan[kThreads - 1];
+    __syncthreads();
+  }
+  const int nsub = 2 * nkeep;  // 64-key sub-tiles
+
+  // Sub-tile `it` = half (it & 1) of kept tile (it >> 1): its K rows and its V^T half are
+  // each HALF contiguous bytes of the packed images, copied verbatim into LDS slot it & 1
+  // by buffer loads into LDS (each lane moves 16 bytes; one wave instruction fills 1 KB in
+  // lane order) over this bank's images, whose byte size bounds the buffer resource.
+  const int bank_bytes = a.tb * G::kTileBytes;
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.kp + (int64_t)bank * a.tb * G::kTileElems), 0, bank_bytes, kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.vp + (int64_t)bank * a.tb * G::kTileElems), 0, bank_bytes, kBufferRsrcWord3);
+  auto image = [&](int it) {  // byte offset of sub-tile `it` within the bank's images
+    const int j = MODE == kModeDense ? (it >> 1) : list[it >> 1];
+    return __builtin_amdgcn_readfirstlane(j * G::kTileBytes + (it & 1) * HALF);
+  };
+  auto copy = [&](__amdgpu_buffer_rsrc_t rs, int off, char* dst) {
+#pragma unroll
+    for (int i = 0; i < NDMA; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rs, (lds_void*)(dst + 16 * kThreads * i + 1024 * wave), 16,
+          16 * kThreads * i + 16 * t, off, 0, 0);
+  };
+  char* const kslot = lds;
+  char* const vslot = lds + 2 * HALF;
+
+  // Query group q of this wave: rows 32 q .. 32 q + 31 of the wave's kRowsPerWave.
+  int row[kGroups], nat[kGroups];
+  bool valid[kGroups];
+#pragma unroll
+  for (int q = 0; q < kGroups; ++q) {
+    row[q] = qt * kBlock + wave * kRowsPerWave + 32 * q + l32;
+    valid[q] = row[q] < a.n_tokens;
+    nat[q] = valid[q] ? a.rowmap[row[q]] : 0;
+  }
+  if (nsub > 0) {
+    copy(krs, image(0), kslot);
+    copy(vrs, image(0), vslot);
+  }
+  if (nsub > 1) copy(krs, image(1), kslot + HALF);
+  u32x4 qreg[kGroups][NS];
+#pragma unroll
+  for (int q = 0; q < kGroups; ++q) {
+    const uint16_t* qrow = a.q + b * a.qsB + h * a.qsH + (int64_t)nat[q] * a.qsN;
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+      qreg[q][s] = valid[q] ? *reinterpret_cast<const u32x4*>(qrow + 16 * s + 8 * g)
+                            : u32x4{0u, 0u, 0u, 0u};
+  }
+  tile_barrier();
+
+  float m[kGroups], lsum[kGroups];
+  f32x16 oacc[kGroups][NDT];
+#pragma unroll
+  for (int q = 0; q < kGroups; ++q) {
+    m[q] = -INFINITY;
+    lsum[q] = 0.0f;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) oacc[q][dt] = f32x16{};
+  }
+  const bool ragged = (a.n_tokens % kBlock) != 0;
+
+  // S^T (64 keys x 32 queries of each group) of the sub-tile whose K image is in `kl`.
+  auto qk = [&](const char* kl, f32x16 (&s)[kGroups][2]) {
+#pragma unroll
+    for (int st = 0; st < NS; ++st)
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        const u32x4 ka = lds_load16(kl, G::k_off(32 * kt + l32, 2 * st + g));
+#pragma unroll
+        for (int q = 0; q < kGroups; ++q)
+          s[q][kt] = T::mfma32(ka, qreg[q][st], st == 0 ? f32x16{} : s[q][kt]);
+      }
+  };
+  // Keys past the sequence end in a sub-tile of the last (ragged) block.
+  auto mask_tail = [&](f32x16 (&s)[kGroups][2], int it) {
+    const int limit = a.n_tokens - ((a.tb - 1) * kBlock + 64 * (it & 1));
+#pragma unroll
+    for (int q = 0; q < kGroups; ++q)
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int rr = 0; rr < 16; ++rr)
+          if (32 * kt + mfma_row(rr, g) >= limit) s[q][kt][rr] = -INFINITY;
+  };
+  // Lazy running-max update of group q from a per-lane candidate: moves only when the row
+  // max grows by more than kRescaleSlack, rescaling O and l.
+  auto update_max = [&](int q, float mx) {
+    const float mt = pair_max(mx) * a.scale_log2;
+    const bool grow = mt > m[q] + kRescaleSlack;
+    if (__any(grow)) {
+      const float mnew = grow ? mt : m[q];
+      const float alpha = __builtin_amdgcn_exp2f(m[q] - mnew);
+      lsum[q] *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) oacc[q][dt] *= alpha;
+      m[q] = mnew;
+    }
+  };
+  auto row_max = [&](f32x16 (&s)[kGroups][2]) {
+#pragma unroll
+    for (int q = 0; q < kGroups; ++q) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int rr = 0; rr < 16; ++rr) mx = __builtin_elementwise_maximum(mx, s[q][kt][rr]);
+      update_max(q, mx);
+    }
+  };
+
+  // One pipeline step, written as slices that the scheduler may not reorder: slice n reads
+  // one LDS fragment (of slice n+2) and issues one MFMA per query group with the fragment
+  // of slice n -- first the 2*NS of S_{it+1} (head-dimension chunk n/2, key tile n%2),
+  // then the 4*NDT of PV_it (P chunk (kt, hh), O^T tile dt) -- plus a fixed share of VALU
+  // work: while S_{it+1} runs, pairs of P_it = exp2(S_it scale log2e - m) values (two exp,
+  // packed for the PV MFMAs); while PV_it runs, the row max over pairs of S_{it+1} scores.
+  // The matrix core then works while the VALU does, instead of one after the other.
+  auto step = [&](int it, f32x16 (&cur)[kGroups][2], f32x16 (&nxt)[kGroups][2], auto mask_tag,
+                  auto next_tag) {
+    constexpr bool kNext = decltype(next_tag)::value;
+    constexpr bool kMask = decltype(mask_tag)::value;
+    if (it + 1 < nsub) copy(vrs, image(it + 1), vslot + ((it + 1) & 1) * HALF);
+    if (it + 2 < nsub) copy(krs, image(it + 2), kslot + (it & 1) * HALF);
+    const char* kl = kslot + ((it + 1) & 1) * HALF;
+    const char* vl = vslot + (it & 1) * HALF;
+    constexpr int NQK = kNext ? 2 * NS : 0;  // S fragments of this step
+    constexpr int NPV = 4 * NDT;             // PV fragments
+    constexpr int NN = NQK + NPV;
+    constexpr int NPAIR = 16 * kGroups;      // P pairs (16 per group)
+    constexpr int PPS = kNext ? (NPAIR + NQK - 1) / NQK : NPAIR;  // P pairs per slice
+    constexpr int MPS = 16 * kGroups / NPV;  // score pairs of the row max per PV slice
+    auto frag = [&](int n) -> u32x4 {
+      if (n < NQK) return lds_load16(kl, G::k_off(32 * (n & 1) + l32, 2 * (n >> 1) + g));
+      const int i = n - NQK;
+      return lds_load16(vl, G::vt_off(32 * (i % NDT) + l32, 2 * (i / NDT) + g));
+    };
+    int limit = 64;
+    if constexpr (kMask) limit = a.n_tokens - ((a.tb - 1) * kBlock + 64 * ((it + 1) & 1));
+    unsigned w[kGroups][2][2][4];
+    float part[kGroups][2];
+    float mx[kGroups];
+#pragma unroll
+    for (int q = 0; q < kGroups; ++q) mx[q] = -INFINITY;
+    u32x4 fr[3];
+    fr[0] = frag(0);
+    fr[1] = frag(1);
+#pragma unroll
+    for (int n = 0; n < NN; ++n) {
+      if (n + 2 < NN) fr[(n + 2) % 3] = frag(n + 2);
+      // P pairs first (the PV MFMAs need them); pair pr is pair pr / kGroups of group
+      // pr % kGroups, so every group's chunk (kt, hh) is complete by the same slice.
+      if (n * PPS < NPAIR) {
+#pragma unroll
+        for (int pr = n * PPS; pr < n * PPS + PPS && pr < NPAIR; ++pr) {
+          const int q = pr % kGroups, pp = pr / kGroups;
+          const int kt = pp >> 3, hh = (pp >> 2) & 1, e = 2 * (pp & 3);
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(cur[q][kt][8 * hh + e], a.scale_log2, -m[q]));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(cur[q][kt][8 * hh + e + 1], a.scale_log2, -m[q]));
+          part[q][kt] = (pp & 7) ? part[q][kt] + (p0 + p1) : p0 + p1;
+          w[q][kt][hh][e >> 1] = pack2<T>(p0, p1);
+        }
+      }
+      if (n < NQK) {
+        const int st = n >> 1, kt = n & 1;
+#pragma unroll
+        for (int q = 0; q < kGroups; ++q)
+          nxt[q][kt] = T::mfma32(fr[n % 3], qreg[q][st], st == 0 ? f32x16{} : nxt[q][kt]);
+      } else {
+        const int i = n - NQK, kt = i / (2 * NDT), hh = (i / NDT) & 1, dt = i % NDT;
+#pragma unroll
+        for (int q = 0; q < kGroups; ++q) {
+          const u32x4 pk = {w[q][kt][hh][0], w[q][kt][hh][1], w[q][kt][hh][2], w[q][kt][hh][3]};
+          oacc[q][dt] = T::mfma32(fr[n % 3], pk, oacc[q][dt]);
+        }
+        if constexpr (kNext) {
+          // Row max over MPS pairs of S_{it+1} scores (pair mp: group mp % kGroups).
+#pragma unroll
+          for (int mp = i * MPS; mp < (i + 1) * MPS; ++mp) {
+            const int q = mp % kGroups, j = 2 * (mp / kGroups), kt2 = j >> 4, rr = j & 15;
+            float s0 = nxt[q][kt2][rr], s1 = nxt[q][kt2][rr + 1];
+            if constexpr (kMask) {
+              if (32 * kt2 + mfma_row(rr, g) >= limit) s0 = -INFINITY;
+              if (32 * kt2 + mfma_row(rr + 1, g) >= limit) s1 = -INFINITY;
+              nxt[q][kt2][rr] = s0;
+              nxt[q][kt2][rr + 1] = s1;
+            }
+            mx[q] = __builtin_elementwise_maximum(mx[q], __builtin_elementwise_maximum(s0, s1));
+          }
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int q = 0; q < kGroups; ++q) {
+      lsum[q] += part[q][0] + part[q][1];
+      if constexpr (kNext) update_max(q, mx[q]);
+    }
+    tile_barrier();
+  };
+
+  // The last kept tile holds the ragged keys when it is the sequence's last block.
+  const bool ragged_last = ragged && nkeep > 0 &&
+                           (MODE == kModeDense ? true : list[nkeep - 1] == a.tb - 1);
+  const int plain = ragged_last ? nsub - 2 : nsub;  // sub-tiles below this need no mask
+  f32x16 sa[kGroups][2], sb[kGroups][2];
+  if (nsub > 0) {
+    qk(kslot, sa);
+    if (plain == 0) mask_tail(sa, 0);
+    row_max(sa);
+    tile_barrier();  // step 0 overwrites K slot 0 (read just now)
+  }
+  using F = std::false_type;
+  using Tr = std::true_type;
+  // nsub is even, so steps go in pairs (even step: S in sa -> sb, odd step: sb -> sa) and
+  // each array keeps one role.  The last two pairs are peeled: they compute S of the last
+  // kept tile, which is masked when it is the ragged final block, and the final step has
+  // no next sub-tile.
+  int it = 0;
+  for (; it + 4 < nsub; it += 2) {
+    step(it, sa, sb, F{}, Tr{});
+    step(it + 1, sb, sa, F{}, Tr{});
+  }
+  if (nsub >= 4) {
+    step(it, sa, sb, F{}, Tr{});
+    if (ragged_last) step(it + 1, sb, sa, Tr{}, Tr{}); else step(it + 1, sb, sa, F{}, Tr{});
+    it += 2;
+  }
+  if (nsub >= 2) {
+    if (ragged_last) step(it, sa, sb, Tr{}, Tr{}); else step(it, sa, sb, F{}, Tr{});
+    step(it + 1, sb, sa, F{}, F{});
+  }
+
+#pragma unroll
+  for (int q = 0; q < kGroups; ++q) {
+    const float lt = pair_sum(lsum[q]);  // lanes l and l ^ 32 share one row: both valid or not
+    if (valid[q]) store_rows<T, D, MODE>(a, bank, b, h, row[q], nat[q], g, oacc[q], m[q], lt);
+  }
+}
+
 template <class T, int D>
 static hipError_t launch_attention(const AttnArgs& a, int mode, hipStream_t s) {
-  const dim3 grid((unsigned)(a.banks * a.tb)), block(256);
+  const dim3 grid((unsigned)(a.banks * a.tb)), block(kThreads);
   switch (mode) {
     case kModeHead: hipLaunchKernelGGL((attention_kernel<T, D, kModeHead>), grid, block, 0, s, a); break;
     case kModeDense: hipLaunchKernelGGL((attention_kernel<T, D, kModeDense>), grid, block, 0, s, a); break;

@@ -115,6 +115,20 @@ __device__ inline int xcd_linear(int bid, int n) {
   return xcd * per + min(xcd, rem) + slot;
 }
 
+// Work-item order for kernels whose items share data with their neighbours: items go to
+// the XCDs in runs of `run` consecutive items (run 0 to XCD 0, run 1 to XCD 1, ...), so the
+// items in flight on one XCD are neighbours (shared tiles stay in that XCD's L2) while all
+// XCDs together stay within 8 * run consecutive items (one working set in the Infinity
+// Cache).  The items left after the last full round of 8 runs are dealt round-robin.  The
+// map is a bijection of [0, n).
+__host__ __device__ inline int xcd_runs(int bid, int n, int run) {
+  const int round = 8 * run;
+  const int full = n / round * round;
+  if (bid >= full) return bid;  // round-robin tail: identity keeps XCD i % 8
+  const int xcd = bid & 7, slot = bid >> 3;
+  return (slot / run * 8 + xcd) * run + slot % run;
+}
+
 // Packed tile geometry.  A K tile is [128 keys][D] with its 16-byte chunks XOR-swizzled by
 // key row.  A V^T tile is two halves (keys 0-63, 64-127), each [D][64 positions] with
 // 128-byte rows whose chunks are swizzled by d row; position p of the tile holds key

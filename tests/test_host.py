@@ -89,6 +89,25 @@ def test_geometry_matches_reference_shapes():
     assert wan.counts("cpu")[-1] == 120
 
 
+def test_xcd_runs_is_a_bijection_keeping_runs_on_one_xcd():
+    # Host restatement of the attention work-item remap in csrc/common.hpp (xcd_runs):
+    # workgroup b runs on XCD b % 8; in the full rounds every run of `run` consecutive items
+    # lands on one XCD, and run r on XCD r % 8.
+    def remap(bid, n, run):
+        full = n // (8 * run) * (8 * run)
+        if bid >= full:
+            return bid
+        xcd, slot = bid & 7, bid >> 3
+        return (slot // run * 8 + xcd) * run + slot % run
+
+    for n in (1, 7, 8, 513, 931, 22344, 931 * 24 + 5):
+        for run in (1, 16, 64):
+            items = [remap(b, n, run) for b in range(n)]
+            assert sorted(items) == list(range(n))
+            full = n // (8 * run) * (8 * run)
+            assert all((items[b] // run) % 8 == b % 8 for b in range(full))
+
+
 def test_xcd_linear_is_a_bijection():
     # Host restatement of the device work-item remap in csrc/common.hpp.
     for n in (1, 7, 8, 9, 22344, 931 * 24 + 5):
