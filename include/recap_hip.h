@@ -106,8 +106,11 @@ int recap_closure_stats(const void* k_tiles, const void* vt_tiles, const float* 
 int recap_partial_reduce(const float* partial, int64_t banks, int64_t groups, int64_t elems,
                          float divisor, float* out, void* stream);
 
-/* Query-type tables of the coarse tail, [banks, nb, dim] each: w = fold_rank(variance,
- * rank) with columns stored in swap23 order, kbar, vbar.
+/* Query-type tables of the coarse tail: w = fold_rank(variance, rank) (columns in swap23
+ * order), kbar, vbar, each written as tile images of 32 key blocks, [banks, ceil(nb/32)*32,
+ * dim] elements (rows past nb zero): kbar and w tiles in the packed K-tile layout, vbar
+ * tiles transposed ([dim][32 positions], position p holding block swap23(p)), so the
+ * coarse tail copies a tile verbatim into LDS.
  * Replaces fold_rank (recap/sparse/closure.py:96-104) and the casts of
  * recap/kernels/coarse_tail.py:238-241. */
 int recap_coarse_tables(const float* variance, const float* k_means, const float* v_means,
@@ -123,7 +126,8 @@ int recap_basis_tables(const float* basis, const float* cvk, int dtype, int64_t 
                        void* stream);
 
 /* Corrected coarse tail for the R refined rows: go [banks, R, dim] (query type),
- * gl [banks, R] fp32; with glref [banks, R] also drift_partial [banks, R/128].
+ * gl [banks, R] fp32; with glref [banks, R] also drift_partial [banks, R/128].  kbar, vbar
+ * and w are the tile images written by recap_coarse_tables.
  * Replaces coarse_tail_attention + _coarse_tail_kernel (recap/kernels/coarse_tail.py:
  * 35-312), build_coarse_tail_plan (recap/sparse/planner.py:11-38), rotated_query_square
  * and value_drift (recap/sparse/closure.py:84-93) and coarse_tail_apply

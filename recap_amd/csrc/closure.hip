@@ -218,13 +218,22 @@ hipError_t run_partial_reduce(const float* part, int banks, int groups, int elem
   return hipGetLastError();
 }
 
-template <class T>
+// One workgroup per padded table row (bank, j), j < ntiles * 32: fold_rank of the rotated
+// variance (recap/sparse/closure.py:96-104), then w, kbar, vbar rounded to the query type
+// and written into their tile images (rows j >= nb are zero).
+template <class T, int D>
 __global__ __launch_bounds__(128) void tables_kernel(TablesArgs a) {
+  using G = TileGeom<D>;
   __shared__ float red[128];
   __shared__ float vals[128];
-  const int64_t row = blockIdx.x;  // bank * nb + j
-  const int t = threadIdx.x, D = a.dim;
-  const float v = t < D ? a.var[row * D + t] : 0.0f;
+  const int ntiles = (a.nb + kCoarseSlots - 1) / kCoarseSlots;
+  const int bank = blockIdx.x / (ntiles * kCoarseSlots);
+  const int j = blockIdx.x % (ntiles * kCoarseSlots);
+  const int tile = j / kCoarseSlots, slot = j % kCoarseSlots;
+  const bool real = j < a.nb;
+  const int64_t row = (int64_t)bank * a.nb + j;
+  const int t = threadIdx.x;
+  const float v = (real && t < D) ? a.var[row * D + t] : 0.0f;
   const bool fold = a.rank > 0 && a.rank < D;
   red[t] = (fold && t >= a.rank && t < D) ? v : 0.0f;
   __syncthreads();
@@ -236,16 +245,28 @@ __global__ __launch_bounds__(128) void tables_kernel(TablesArgs a) {
   vals[t] = (fold && t >= a.rank) ? residual : v;
   __syncthreads();
   if (t < D) {
-    a.w_t[row * D + t] = T::from_f(vals[swap23(t)]);
-    a.kbar_t[row * D + t] = T::from_f(a.kmean[row * D + t]);
-    a.vbar_t[row * D + t] = T::from_f(a.vmean[row * D + t]);
+    const int64_t tile_base = ((int64_t)bank * ntiles + tile) * kCoarseSlots * D * 2;  // bytes
+    const int koff = G::k_off(slot, t >> 3) + ((t & 7) << 1);
+    const uint16_t wv = real ? T::from_f(vals[swap23(t)]) : (uint16_t)0;
+    const uint16_t kv = real ? T::from_f(a.kmean[row * D + t]) : (uint16_t)0;
+    const uint16_t vv = real ? T::from_f(a.vmean[row * D + t]) : (uint16_t)0;
+    *reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(a.w_t) + tile_base + koff) = wv;
+    *reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(a.kbar_t) + tile_base + koff) = kv;
+    *reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(a.vbar_t) + tile_base +
+                                 coarse_vt_off(t, swap23(slot))) = vv;
   }
 }
 
 hipError_t run_tables(const TablesArgs& a, int dtype, hipStream_t s) {
-  const dim3 grid((unsigned)(a.banks * a.nb)), block(128);
-  if (dtype == BF16::code) hipLaunchKernelGGL(tables_kernel<BF16>, grid, block, 0, s, a);
-  else hipLaunchKernelGGL(tables_kernel<F16>, grid, block, 0, s, a);
+  const int ntiles = (a.nb + kCoarseSlots - 1) / kCoarseSlots;
+  const dim3 grid((unsigned)(a.banks * ntiles * kCoarseSlots)), block(128);
+  if (dtype == BF16::code) {
+    if (a.dim == 128) hipLaunchKernelGGL((tables_kernel<BF16, 128>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((tables_kernel<BF16, 64>), grid, block, 0, s, a);
+  } else {
+    if (a.dim == 128) hipLaunchKernelGGL((tables_kernel<F16, 128>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((tables_kernel<F16, 64>), grid, block, 0, s, a);
+  }
   return hipGetLastError();
 }
 

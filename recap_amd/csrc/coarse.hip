@@ -6,15 +6,16 @@
 //   drift = s C_vk q       in the query type  (recap/sparse/closure.py:89-93)
 //   l_j   = s q.kbar_j + ln n_j + [s^2 qsq.w_j <= theta^2] (s^2/2) qsq.w_j
 //   out   = softmax(l) . vbar  (+ g * drift, g = gated share of the mass), lse = m + ln l
-// over the omitted blocks j (~partition[i, j]); the omitted list is compacted in LDS
-// from the partition row, so no host-side planning or synchronisation is needed
-// (recap/sparse/planner.py:24-27 is the host sync this removes).
+// over the omitted blocks j (~partition[i, j]), walked in 32-block tiles of the tables with
+// the partition row as a bit mask (tiles without an omitted block are skipped), so no
+// host-side planning or synchronisation is needed (recap/sparse/planner.py:24-27 is the
+// host sync this removes).
 //
 // One workgroup = one (bank, 128-row query block), 4 waves x 32 rows.  The three
 // contractions per 32-block tile (q.kbar, qsq.w, p.vbar) run on 32x32x16 MFMA with the
 // same register-resident layout trick as the attention kernel: the fp32 result of one
-// MFMA is the B operand of the next, and the tables' columns (w) or rows (vbar^T in LDS)
-// are stored in the matching swap23 order.  Also writes per-block partial sums of
+// MFMA is the B operand of the next, and the tables' columns (w) or rows (vbar^T) are
+// stored in the matching swap23 order, as tile images copied verbatim into LDS.  Also writes per-block partial sums of
 // (gl - gl_ref) for the per-bank drift centre (recap/operator.py:148-150).
 #include "kernels.hpp"
 
@@ -22,44 +23,41 @@ namespace recap {
 
 constexpr int kMaxVideoBlocks = 4096;
 
+typedef __attribute__((address_space(3))) void lds_void;
+constexpr int kBufferRsrcWord3 = 0x00020000;  // raw buffer resource word 3 on CDNA
+constexpr float kTailSlack = 8.0f * kLn2;      // lazy-max slack, natural-log units
+
 template <class T, int D>
 __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
 #pragma clang fp contract(off)
   using G = TileGeom<D>;
   constexpr int NS = D / 16, NDT = D / 32, NCH = D / 8;
   constexpr int kMatBytes = D * D * 2;
-  constexpr int kTabBytes = 32 * D * 2;
-  constexpr int kBuf = kMatBytes > 3 * kTabBytes ? kMatBytes : 3 * kTabBytes;
+  constexpr int kTabBytes = kCoarseSlots * D * 2;  // one table tile image
+  constexpr int kStage = 3 * kTabBytes;            // the kbar, w, vbar tiles of one tile
+  constexpr int kBuf = kMatBytes > 2 * kStage ? kMatBytes : 2 * kStage;
+  constexpr int NDMA = kTabBytes / 4096;           // 16-byte copies per thread per image
   __shared__ __attribute__((aligned(16))) char buf[kBuf];
-  __shared__ uint16_t list[kMaxVideoBlocks];
-  __shared__ int scan[256];
+  __shared__ unsigned omit[kMaxVideoBlocks / kCoarseSlots];
   __shared__ float wsum[4];
 
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, g = lane >> 5, l32 = lane & 31;
+  const int t = threadIdx.x, lane = t & 63, g = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int lin = xcd_linear(blockIdx.x, a.banks * a.qtiles);
   const int bank = lin / a.qtiles, qt = lin % a.qtiles;
   const int b = bank / a.heads, h = bank % a.heads;
+  const int ntiles = (a.nb + kCoarseSlots - 1) / kCoarseSlots;
 
-  // Omitted blocks of this query block, in increasing order.
-  int n_omit;
+  // Omitted blocks of this query block (partition 0) as one bit word per table tile.
   {
     const uint8_t* prow = a.partition + ((int64_t)bank * a.nb + qt) * a.nb;
-    const int per = (a.nb + 255) / 256;
-    const int j0 = min(t * per, a.nb), j1 = min(j0 + per, a.nb);
-    int cnt = 0;
-    for (int j = j0; j < j1; ++j) cnt += prow[j] == 0;
-    scan[t] = cnt;
-    __syncthreads();
-    for (int off = 1; off < 256; off <<= 1) {
-      const int v = t >= off ? scan[t - off] : 0;
-      __syncthreads();
-      scan[t] += v;
-      __syncthreads();
+    for (int base = 0; base < ntiles * kCoarseSlots; base += 256) {
+      const int j = base + t;
+      const unsigned long long bal = __ballot(j < a.nb && prow[j] == 0);
+      const int wi = (base + 64 * wave) / kCoarseSlots;
+      if (lane == 0 && wi < ntiles) omit[wi] = (unsigned)bal;
+      if (lane == 0 && wi + 1 < ntiles) omit[wi + 1] = (unsigned)(bal >> 32);
     }
-    int pos = scan[t] - cnt;
-    for (int j = j0; j < j1; ++j)
-      if (prow[j] == 0) list[pos++] = (uint16_t)j;
-    n_omit = scan[255];
   }
 
   // Stage U^T (query type, [D][D]) into LDS.
@@ -102,6 +100,7 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
       qsq_pk[ot][hh] = u32x4{w[0], w[1], w[2], w[3]};
     }
   }
+  __syncthreads();  // the table tiles reuse the U^T staging area
 
   const float s32 = a.scale;
   const float ssq = (float)((double)a.scale * (double)a.scale);
@@ -110,37 +109,53 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
   const float ln_full = logf((float)kBlock);
   const float ln_last = logf((float)(a.n_video - kBlock * (a.nb - 1)));
 
-  char* kb_lds = buf;
-  char* w_lds = buf + kTabBytes;
-  char* vt_lds = buf + 2 * kTabBytes;
+  // Table tiles (images written by the tables kernel) are copied verbatim into LDS, one
+  // tile ahead, by buffer loads over this bank's images; tiles with no omitted block are
+  // skipped.
+  const int bank_tab = ntiles * kTabBytes;
+  const int64_t tab_elems = (int64_t)bank * ntiles * kCoarseSlots * D;
+  const __amdgpu_buffer_rsrc_t krs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(a.kbar + tab_elems), 0, bank_tab, kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t wrs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(a.w + tab_elems), 0, bank_tab, kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t vrs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(a.vbar + tab_elems), 0, bank_tab, kBufferRsrcWord3);
+  auto copy_tile = [&](int k, int stage) {
+    char* dst = buf + stage * kStage;
+    const int off = __builtin_amdgcn_readfirstlane(k * kTabBytes);
+#pragma unroll
+    for (int i = 0; i < NDMA; ++i) {
+      const int lo = 4096 * i + 1024 * wave, vo = 4096 * i + 16 * t;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void*)(dst + lo), 16, vo, off, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_void*)(dst + kTabBytes + lo), 16, vo, off, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void*)(dst + 2 * kTabBytes + lo), 16, vo, off, 0, 0);
+    }
+  };
+  auto next_tile = [&](int k) {
+    ++k;
+    while (k < ntiles && omit[k] == 0) ++k;
+    return k;
+  };
+
   float m = -INFINITY, lsum = 0.0f, gsum = 0.0f;
   f32x16 oacc[NDT];
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) oacc[dt] = f32x16{};
 
-  for (int base = 0; base < n_omit; base += 32) {
-    __syncthreads();
-    for (int cc = t; cc < 32 * NCH; cc += 256) {
-      const int slot = cc / NCH, c = cc % NCH;
-      const bool valid = base + slot < n_omit;
-      const int64_t row = (int64_t)bank * a.nb + (valid ? list[base + slot] : 0);
-      const u32x4 zero = {0u, 0u, 0u, 0u};
-      const u32x4 kv = valid ? *reinterpret_cast<const u32x4*>(a.kbar + row * D + 8 * c) : zero;
-      const u32x4 wv = valid ? *reinterpret_cast<const u32x4*>(a.w + row * D + 8 * c) : zero;
-      const u32x4 vv = valid ? *reinterpret_cast<const u32x4*>(a.vbar + row * D + 8 * c) : zero;
-      *reinterpret_cast<u32x4*>(kb_lds + G::k_off(slot, c)) = kv;
-      *reinterpret_cast<u32x4*>(w_lds + G::k_off(slot, c)) = wv;
-      const int pos = swap23(slot);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int d = 8 * c + e;
-        const uint16_t hv = (uint16_t)((e & 1) ? vv[e >> 1] >> 16 : vv[e >> 1] & 0xffff);
-        const int off = d * 64 + ((((pos >> 3) ^ ((d >> 2) & 3))) << 4) + ((pos & 7) << 1);
-        *reinterpret_cast<uint16_t*>(vt_lds + off) = hv;
-      }
-    }
-    __syncthreads();
+  int k = next_tile(-1), stage = 0;
+  if (k < ntiles) copy_tile(k, 0);
+  while (k < ntiles) {
+    // This wave's copies of tile k have landed and every wave is done with the other stage.
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0x7 << 4);  // vmcnt(0) lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    const int kn = next_tile(k);
+    if (kn < ntiles) copy_tile(kn, stage ^ 1);
 
+    const char* kb_lds = buf + stage * kStage;
+    const char* w_lds = kb_lds + kTabBytes;
+    const char* vt_lds = kb_lds + 2 * kTabBytes;
     f32x16 sacc = f32x16{}, wacc = f32x16{};
 #pragma unroll
     for (int s = 0; s < NS; ++s) sacc = T::mfma32(lds_load16(kb_lds, G::k_off(l32, 2 * s + g)), qreg[s], sacc);
@@ -150,42 +165,45 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
       for (int hh = 0; hh < 2; ++hh)
         wacc = T::mfma32(lds_load16(w_lds, G::k_off(l32, 4 * ot + 2 * hh + g)), qsq_pk[ot][hh], wacc);
 
+    // Lane (g, l32) holds slots mfma_row(rr, g): bits 8 (rr / 4) + 4 g + rr % 4 of the word.
+    // Kept blocks get -inf (branch-free selects).
+    const unsigned lb = omit[k] >> (4 * g);
     float sc[16];
     bool gate[16];
     float mx = -INFINITY;
 #pragma unroll
     for (int rr = 0; rr < 16; ++rr) {
-      const int idx = base + mfma_row(rr, g);
-      if (idx < n_omit) {
-        const int j = list[idx];
-        float v = sacc[rr] * s32;
-        v = v + (j == a.nb - 1 ? ln_last : ln_full);
-        const float quad = wacc[rr];
-        gate[rr] = quad * ssq <= thsq;
-        v = v + (gate[rr] ? quad * half : 0.0f);
-        sc[rr] = v;
-      } else {
-        sc[rr] = -INFINITY;
-        gate[rr] = false;
-      }
-      mx = fmaxf(mx, sc[rr]);
+      const bool om = (lb >> (8 * (rr >> 2) + (rr & 3))) & 1u;
+      const int j = kCoarseSlots * k + mfma_row(rr, g);
+      const float quad = wacc[rr];
+      const bool gt = om && quad * ssq <= thsq;
+      float v = sacc[rr] * s32;
+      v = v + (j == a.nb - 1 ? ln_last : ln_full);
+      v = v + (gt ? quad * half : 0.0f);
+      sc[rr] = om ? v : -INFINITY;
+      gate[rr] = gt;
+      mx = __builtin_elementwise_maximum(mx, sc[rr]);
     }
+    // Lazy running max: moves only when it grows by more than kTailSlack (p stays < 2^8).
     mx = pair_max(mx);
-    const float mnew = fmaxf(m, mx);
-    const float alpha = expf(m - mnew);
-    lsum *= alpha;
-    gsum *= alpha;
+    const bool grow = mx > m + kTailSlack;
+    if (__any(grow)) {
+      const float mnew = grow ? mx : m;
+      const float alpha = __builtin_amdgcn_exp2f((m - mnew) * kLog2e);
+      lsum *= alpha;
+      gsum *= alpha;
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) oacc[dt] *= alpha;
-    m = mnew;
+      for (int dt = 0; dt < NDT; ++dt) oacc[dt] *= alpha;
+      m = mnew;
+    }
     u32x4 pk[2];
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       unsigned w[4];
 #pragma unroll
       for (int e = 0; e < 8; e += 2) {
-        const float p0 = expf(sc[8 * hh + e] - mnew);
-        const float p1 = expf(sc[8 * hh + e + 1] - mnew);
+        const float p0 = __builtin_amdgcn_exp2f((sc[8 * hh + e] - m) * kLog2e);
+        const float p1 = __builtin_amdgcn_exp2f((sc[8 * hh + e + 1] - m) * kLog2e);
         lsum += p0;
         lsum += p1;
         gsum += gate[8 * hh + e] ? p0 : 0.0f;
@@ -198,11 +216,11 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
     for (int dt = 0; dt < NDT; ++dt) {
       const int d = 32 * dt + l32;
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const int off = d * 64 + ((((2 * hh + g) ^ ((d >> 2) & 3))) << 4);
-        oacc[dt] = T::mfma32(lds_load16(vt_lds, off), pk[hh], oacc[dt]);
-      }
+      for (int hh = 0; hh < 2; ++hh)
+        oacc[dt] = T::mfma32(lds_load16(vt_lds, coarse_vt_off(d, 8 * (2 * hh + g))), pk[hh], oacc[dt]);
     }
+    k = kn;
+    stage ^= 1;
   }
 
   // Value drift s C_vk q in the output layout: stage C_vk over the tables' LDS.

@@ -157,6 +157,15 @@ struct TileGeom {
   }
 };
 
+// Coarse-tail table tiles: 32 key blocks (slots) per tile.  K-bar and w tiles are K-tile
+// rows (TileGeom<D>::k_off with the slot as the row); the V-bar tile is transposed,
+// [D][32 positions] with 64-byte rows, position p holding slot swap23(p), and 16-byte chunks
+// XOR-swizzled by bits 2-3 of the row.
+constexpr int kCoarseSlots = 32;
+__host__ __device__ inline int coarse_vt_off(int d, int pos) {  // bytes
+  return d * 64 + (((pos >> 3) ^ ((d >> 2) & 3)) << 4) + ((pos & 7) << 1);
+}
+
 __device__ inline u32x4 lds_load16(const char* base, int off) {
   return *reinterpret_cast<const u32x4*>(base + off);
 }

@@ -240,10 +240,15 @@ def basis_tables(basis: torch.Tensor | None, cvk: torch.Tensor | None, dtype: to
     return out
 
 
+COARSE_SLOTS = 32  # key blocks per coarse-tail table tile
+
+
 def coarse_tables(var: torch.Tensor, kv: PackedKV, rank: int):
+    """w, kbar, vbar as tile images [banks, ceil(nb/32)*32, d] (see recap_coarse_tables)."""
     var = var.to(torch.float32).contiguous()
     banks, nb, d = var.shape
-    mk = lambda: torch.empty(banks, nb, d, dtype=kv.dtype, device=var.device)  # noqa: E731
+    padded = -(-nb // COARSE_SLOTS) * COARSE_SLOTS
+    mk = lambda: torch.empty(banks, padded, d, dtype=kv.dtype, device=var.device)  # noqa: E731
     w, kbar, vbar = mk(), mk(), mk()
     call("recap_coarse_tables", var.data_ptr(), kv.k_means.data_ptr(), kv.v_means.data_ptr(),
          dtype_code(kv.dtype), banks, nb, d, int(rank), w.data_ptr(), kbar.data_ptr(),
