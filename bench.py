@@ -27,6 +27,10 @@ sys.path.insert(0, str(ROOT))
 METRIC = "ms per corrected sparse-attn call @Hunyuan 720p shape; eff. TFLOP/s vs dense"
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
+# HBM bytes per launch of the attention kernel, measured with rocprofv3 FETCH_SIZE and
+# WRITE_SIZE passes scaled by a plain copy of known size (the file records the commands).
+TRAFFIC_FILE = ROOT / "profiles" / "attention_hunyuan720p_traffic.md"
+COPY_CAL_BYTES = 1 << 30
 
 
 def log(msg: str) -> None:
@@ -50,6 +54,32 @@ def elapsed_stages(events: dict) -> dict:
         pairs = list(zip(events[a], events[b]))
         out[b] = sum(s.elapsed_time(e) for s, e in pairs) / len(pairs)
     return out
+
+
+def recorded_traffic(workload: str) -> float | None:
+    """HBM bytes per attention launch from the committed rocprof summary, if it covers
+    this workload (a line 'traffic_bytes_per_launch <workload> <bytes>')."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        parts = line.strip().strip("`").split()
+        if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == workload:
+            return float(parts[2])
+    return None
+
+
+def copy_calibration(reps: int = 5) -> int:
+    """A plain device copy of COPY_CAL_BYTES, the known-size reference for the FETCH_SIZE /
+    WRITE_SIZE counters: each dispatch reads and writes exactly COPY_CAL_BYTES."""
+    import torch
+    x = torch.empty(COPY_CAL_BYTES // 2, dtype=torch.bfloat16, device="cuda").normal_()
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": COPY_CAL_BYTES, "dispatches": reps}), flush=True)
+    return 0
 
 
 def cpu_baseline(op, q1, k1, v1, wl, heads: int) -> dict:
@@ -114,6 +144,8 @@ def main() -> int:
                     help="heads of the CPU baseline sample (0 = skip)")
     ap.add_argument("--profile", action="store_true",
                     help="only the sparse calls (no dense comparator, no CPU baseline)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain 1 GiB device copy (counter calibration under rocprofv3)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: --gpus {args.gpus} is not supported in this build "
@@ -121,11 +153,15 @@ def main() -> int:
               "measured here)", file=sys.stderr)
         return 2
 
+    if args.copy_calibration:
+        return copy_calibration()
+
     import torch
     import torch.nn.functional as F
 
     from recap_amd import Operator, OperatorConfig, REFRESH, SPARSE
     from recap_amd import _lib
+    from recap_amd import kernels as K
     from recap_amd.layout import Layout, SparseGeometry, hilbert_permutation
     from recap_amd.synthetic import WORKLOADS, make_qkv, perturb
 
@@ -162,8 +198,28 @@ def main() -> int:
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps
     stages = elapsed_stages(op.stage_events)
+    ev = op.stage_events
+    per_call = sorted(a.elapsed_time(b) for a, b in zip(ev["start"], ev["attention"]))
+    median_ms = per_call[len(per_call) // 2]
     op.stage_events = None
-    log(f"[bench] sparse call {ms:.3f} ms; stages {stages}")
+    log(f"[bench] sparse call {ms:.3f} ms (median {median_ms:.3f}); stages {stages}")
+
+    # Stage-1 selection (REFRESH-only in the reference) on the same inputs, timed alone so
+    # that "call + fresh selection" can be reported.
+    layer = op.layers[0][0]
+    rowmap = op.layout.rowmap(dev)
+    geo = op._geometry(q1)
+    kv = K.kv_pack(k1, v1, rowmap, geo)
+    op._select(layer, q1, kv, geo, rowmap)
+    torch.cuda.synchronize()
+    s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s0.record()
+    for _ in range(3):
+        op._select(layer, q1, kv, geo, rowmap)
+    s1.record()
+    torch.cuda.synchronize()
+    select_ms = s0.elapsed_time(s1) / 3
+    log(f"[bench] fresh selection {select_ms:.3f} ms")
 
     dense_tflop = wl.dense_flops() / 1e12
     kept = kept_flops(op.banks[0][0].head_kernel_mask, wl.tokens, wl.dim)
@@ -185,6 +241,9 @@ def main() -> int:
         "config": {"workload": wl.name, "batch": 1, "heads": wl.heads, "head_dim": wl.dim,
                    "tokens": wl.tokens, "video_tokens": wl.video_tokens,
                    "text_tokens": wl.text_tokens, "block": 128, "density": wl.density},
+        "median_ms_per_call": round(median_ms, 4),
+        "select_ms": round(select_ms, 4),
+        "ms_per_call_with_fresh_selection": round(ms + select_ms, 4),
         "effective_tflops": round(dense_tflop / (ms / 1e3), 2),
         "dense_equivalent_tflop": round(dense_tflop, 3),
         "kept_block_tflop": round(kept / 1e12, 3),
@@ -195,7 +254,7 @@ def main() -> int:
             "achieved": round(kept / (attn_ms / 1e3) / 1e12, 2),
             "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
             "frac": round(kept / (attn_ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": recorded_traffic(wl.name),
         },
     }
     if not args.profile:
