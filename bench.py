@@ -82,6 +82,87 @@ def copy_calibration(reps: int = 5) -> int:
     return 0
 
 
+def step_sequence(wl, layers: int, steps: int, refresh_at: tuple, drift: float) -> dict:
+    """The multi-step schedule with paged refinement banks (one JSON object).
+
+    Every step runs `layers` attention layers; steps in `refresh_at` are REFRESH, the others
+    SPARSE; inputs drift by `drift` (fresh N(0,1) noise) each step and are shared by the
+    layers (each layer keeps its own banks).  Run twice: banks in pinned host memory paged
+    through two GPU slots with layer-ahead prefetch (HostBankOperator), and banks resident
+    on the GPU (Operator).  copy-overlap fraction = 1 - exposed / total copy time, where
+    total = the HIP-event durations of every host<->device bank copy on its stream and
+    exposed = the paged run's extra time over the resident run."""
+    import torch
+
+    from recap_amd import HostBankOperator, Operator, OperatorConfig, REFRESH, SPARSE
+    from recap_amd.layout import Layout, SparseGeometry, hilbert_permutation
+    from recap_amd.synthetic import make_qkv, perturb
+
+    dev = torch.device("cuda:0")
+    layout = Layout.from_permutation(hilbert_permutation(wl.grid), text_tokens=wl.text_tokens,
+                                     text_first=wl.text_first)
+    geometry = SparseGeometry.build(layout, 128)
+    base = make_qkv(wl, seed=0, device=dev)
+    inputs = []
+    for step in range(steps):
+        base = tuple(perturb(x, drift, seed=i, step=step + 1) for i, x in enumerate(base))
+        inputs.append(base)
+        torch.cuda.synchronize()
+
+    def run(cls, host: bool):
+        cfg = OperatorConfig(head_density=wl.density, host_banks=host)
+        op = cls.build(cfg, geometry, n_layers=layers)
+        if host:
+            op.preallocate_host(layers, wl.heads, wl.dim)
+            op.record_copies = True
+        times, outs = [], None
+        for step in range(steps):
+            kind = REFRESH if step in refresh_at else SPARSE
+            q, k, v = inputs[step]
+            torch.cuda.synchronize()
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            op.begin_step(step, kind)
+            for layer in range(layers):
+                out = op.attend(layer, q, k, v)
+                if layer == layers - 1:
+                    outs = out
+            end.record()
+            torch.cuda.synchronize()
+            times.append((kind, start.elapsed_time(end)))
+            log(f"[sequence] {'host' if host else 'gpu'} banks step {step} {kind}: "
+                f"{times[-1][1]:.1f} ms")
+        copy_ms = 0.0
+        host_bytes = 0
+        if host:
+            copy_ms = sum(a.elapsed_time(b) for _, a, b in op.copy_events)
+            host_bytes = op.peak_bank_bytes()
+            op.finish()
+        del op
+        torch.cuda.empty_cache()
+        return times, copy_ms, host_bytes, outs
+
+    t_host, copy_ms, host_bytes, out_host = run(HostBankOperator, True)
+    t_gpu, _, _, out_gpu = run(Operator, False)
+    total_host = sum(t for _, t in t_host)
+    total_gpu = sum(t for _, t in t_gpu)
+    exposed = max(0.0, total_host - total_gpu)
+    mean = lambda xs: sum(xs) / len(xs) if xs else None  # noqa: E731
+    return {
+        "sequence": f"{wl.name}: {layers} layers x {steps} steps, REFRESH at "
+                    f"{list(refresh_at)}, SPARSE otherwise, {drift:.0%} input drift per step",
+        "ms_per_step_host_banks": round(total_host / steps, 2),
+        "ms_per_step_gpu_banks": round(total_gpu / steps, 2),
+        "ms_per_refresh_step_host_banks": round(mean([t for k, t in t_host if k == REFRESH]), 2),
+        "ms_per_sparse_step_host_banks": round(mean([t for k, t in t_host if k == SPARSE]), 2),
+        "copy_ms_total": round(copy_ms, 2),
+        "exposed_copy_ms": round(exposed, 2),
+        "copy_overlap_fraction": round(1.0 - exposed / copy_ms, 4) if copy_ms > 0 else None,
+        "host_bank_bytes": host_bytes,
+        "outputs_identical": bool(torch.equal(out_host, out_gpu)),
+    }
+
+
 def cpu_baseline(op, q1, k1, v1, wl, heads: int) -> dict:
     """The oracle's sparse call on the host for ``heads`` of the heads (all query blocks),
     timed with the operator's refinement state; heads are independent and cost the same,
@@ -146,6 +227,10 @@ def main() -> int:
                     help="only the sparse calls (no dense comparator, no CPU baseline)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device copy (counter calibration under rocprofv3)")
+    ap.add_argument("--sequence", action="store_true",
+                    help="run only the step sequence with paged banks (20 layers, 10 steps, "
+                         "REFRESH at 0 and 5, 3%% drift) and print its JSON line")
+    ap.add_argument("--layers", type=int, default=20, help="layers of the step sequence")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: --gpus {args.gpus} is not supported in this build "
@@ -168,6 +253,9 @@ def main() -> int:
     _lib.load()
     wl = WORKLOADS[args.workload]
     dev = torch.device("cuda:0")
+    if args.sequence:
+        print(json.dumps(step_sequence(wl, args.layers, 10, (0, 5), 0.03)), flush=True)
+        return 0
     log(f"[bench] workload {wl.name}: heads={wl.heads} d={wl.dim} N={wl.tokens}")
     q0, k0, v0 = make_qkv(wl, seed=0, device=dev)
     q1, k1, v1 = (perturb(x, 0.02, seed=0, step=1) for x in (q0, k0, v0))

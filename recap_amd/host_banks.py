@@ -36,6 +36,7 @@ class HostBankOperator(Operator):
         self._split_slots: dict = {}
         self._device = None
         self._prefetched = None
+        self._split_prefetched = None
         self.copy_events: list[tuple[str, torch.cuda.Event, torch.cuda.Event]] = []
         self.record_copies = False
 
@@ -116,35 +117,53 @@ class HostBankOperator(Operator):
 
     # -- per-layer partition state -------------------------------------------------------
 
-    def _split_in(self, bank, key_id) -> None:
-        host = self._host_split.get(key_id)
-        if not host:
-            return
-        slot = self._split_slots.setdefault(key_id[1] % max(1, len(self._slots)), {})
-        for name, tensor in host.items():
+    def _split_slot(self, key_id) -> dict:
+        return self._split_slots.setdefault(key_id[1] % max(1, len(self._slots)), {})
+
+    def _copy_split(self, key_id, stream=None) -> dict:
+        """Copy the layer's partition, kernel mask and drift reference into its split slot
+        (recap/host_banks.py:116-130) on `stream` (default: the current stream)."""
+        slot = self._split_slot(key_id)
+        for name, tensor in self._host_split.get(key_id, {}).items():
             dev = slot.get(name)
             if dev is None or dev.shape != tensor.shape or dev.dtype != tensor.dtype:
                 dev = torch.empty(tensor.shape, dtype=tensor.dtype, device=self._device)
                 slot[name] = dev
-            K.bank_copy_async(dev, tensor)
-            setattr(bank, name, dev)
+            K.bank_copy_async(dev, tensor, stream)
+        return slot
+
+    def _split_in(self, bank, key_id) -> None:
+        if not self._host_split.get(key_id):
+            return
+        if self._split_prefetched == key_id:
+            slot = self._split_slot(key_id)  # copied with the bank on the prefetch stream
+            self._split_prefetched = None
+        else:
+            slot = self._copy_split(key_id)
+        for name in self._host_split[key_id]:
+            setattr(bank, name, slot[name])
 
     def _split_out(self, bank, key_id) -> None:
+        """Queue the layer's split state (partition, kernel mask, drift reference) for its
+        pinned host buffers on the current stream, which is the write-back stream when
+        called from _stage_out.  The reference copies it synchronously
+        (recap/host_banks.py:132-146); here the slot event that fences the bank write-back
+        also fences these copies, and record_stream keeps the device tensors alive until
+        they are done."""
         host = self._host_split.setdefault(key_id, {})
-        copied = False
+        stream = torch.cuda.current_stream()
         for name in _SPLIT_FIELDS:
             tensor = getattr(bank, name, None)
             if tensor is None:
                 host.pop(name, None)
                 continue
+            tensor = tensor.contiguous()
             buf = host.get(name)
             if buf is None or buf.shape != tensor.shape or buf.dtype != tensor.dtype:
                 buf = torch.empty(tensor.shape, dtype=tensor.dtype, pin_memory=True)
                 host[name] = buf
-            K.bank_copy_async(buf, tensor.contiguous())
-            copied = True
-        if copied:  # the reference copies the split state synchronously
-            torch.cuda.current_stream().synchronize()
+            K.bank_copy_async(buf, tensor, stream)
+            tensor.record_stream(stream)
 
     @staticmethod
     def _split_detach(bank) -> None:
@@ -183,8 +202,7 @@ class HostBankOperator(Operator):
             out = super().attend(layer_index, query, key, value)
         finally:
             if self.kind == REFRESH:
-                self._stage_out(key_id, slot, index)
-                self._split_out(bank, key_id)
+                self._stage_out(key_id, slot, index, bank)
             self._split_detach(bank)
             released = torch.cuda.Event()
             released.record()
@@ -202,29 +220,48 @@ class HostBankOperator(Operator):
         self._maybe_prefetch(key_id)
 
     def _maybe_prefetch(self, key_id) -> None:
+        """Start copying the next layer's bank and split state into the other slot while
+        this layer computes (recap/host_banks.py:209-225).  After the stream's last layer
+        the next one is layer 0 of the following step, when it uses the other slot.  The
+        split state rides along here; the reference copies it on the compute stream.  The
+        slot's write-back event stays set, so a fallback synchronous copy still waits."""
         if self._prefetch_stream is None:
             return
         stream, layer = key_id
         nxt = (stream, layer + 1)
         if nxt not in self._host:
-            return
-        index = (layer + 1) % len(self._slots)
-        if self._slot_ready[index] is not None:
+            nxt = (stream, 0)
+            if layer == 0 or nxt not in self._host:
+                return
+        index = nxt[1] % len(self._slots)
+        if index == layer % len(self._slots):
             return
         with torch.cuda.stream(self._prefetch_stream):
             released = self._slot_free[index]
             if released is not None:
                 self._prefetch_stream.wait_event(released)
+            # A refresh's write-back of the slot must finish reading it first (the
+            # reference skips the prefetch instead, so refresh steps never overlap).
+            written = self._slot_ready[index]
+            if written is not None:
+                self._prefetch_stream.wait_event(written)
             self._copy(self._slots[index], self._host[nxt], "h2d-prefetch")
+            if self._host_split.get(nxt):
+                self._copy_split(nxt, self._prefetch_stream)
+                self._split_prefetched = nxt
         self._prefetched = nxt
 
-    def _stage_out(self, key_id, slot: dict, index: int) -> None:
+    def _stage_out(self, key_id, slot: dict, index: int, bank) -> None:
+        """Copy the new refinement and split state to host memory on the write-back stream
+        after the compute that produced them (recap/host_banks.py:227-242); the slot event
+        fences every later reuse of the slot and of the host buffers."""
         host = self._host_bank(key_id)
         written = torch.cuda.Event()
         written.record()
         with torch.cuda.stream(self._out_stream):
             self._out_stream.wait_event(written)
             self._copy(host, slot, "d2h")
+            self._split_out(bank, key_id)
             event = torch.cuda.Event()
             event.record()
         self._slot_ready[index] = event
@@ -244,6 +281,7 @@ class HostBankOperator(Operator):
         self._slot_ready = [None, None]
         self._slot_free = [None, None]
         self._prefetched = None
+        self._split_prefetched = None
 
     def reset(self) -> None:
         self.finish()

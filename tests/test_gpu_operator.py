@@ -159,6 +159,38 @@ def test_non_contiguous_inputs_and_exact_kind(cuda):
 # -- full HunyuanVideo-720p shape: size-independent properties ----------------------------
 
 
+@pytest.mark.parametrize("layers", [3, 4])
+def test_host_banks_multi_step_schedule_identical(cuda, layers):
+    """REFRESH, SPARSE, SPARSE, REFRESH (re-scoring valid banks), SPARSE, SPARSE over odd and
+    even layer counts: pinned host banks with and without prefetch give the same outputs
+    and validation statistics as banks resident on the GPU, call by call."""
+    wl = SMALL["text-last-d128"]
+    base = make_qkv(wl, seed=2, device=cuda)
+    schedule = [REFRESH, SPARSE, SPARSE, REFRESH, SPARSE, SPARSE]
+    inputs = [tuple(perturb(x, 0.03, seed=i, step=step) for i, x in enumerate(base))
+              for step in range(len(schedule))]
+    runs = {}
+    for label, kw in [("gpu", {}), ("host", {"host_banks": True}),
+                      ("host-noprefetch", {"host_banks": True, "prefetch": False})]:
+        op, _ = build(wl, layers=layers, **kw)
+        outs, stats = [], []
+        for step, kind in enumerate(schedule):
+            op.begin_step(step, kind)
+            for layer in range(layers):
+                outs.append(op.attend(layer, *inputs[step]).clone())
+            if kind == REFRESH:
+                stats.append(op.drain_validation())
+        if hasattr(op, "finish"):
+            op.finish()
+        torch.cuda.synchronize()
+        runs[label] = (outs, stats)
+    for label in ("host", "host-noprefetch"):
+        for i, (a, b) in enumerate(zip(runs["gpu"][0], runs[label][0])):
+            assert torch.equal(a, b), (label, i)
+        assert runs["gpu"][1] == runs[label][1], label
+    assert runs["gpu"][1][1] is not None  # the second refresh scored the first refinement
+
+
 @pytest.fixture(scope="module")
 def hunyuan_inputs(cuda):
     wl = WORKLOADS["hunyuan-720p"]
