@@ -25,9 +25,11 @@ from .host_banks import HostBankOperator
 from .layout import Layout, SparseGeometry, hilbert_permutation
 from .operator import EXACT, REFRESH, SPARSE, DetailBank, Operator, SparseAttention
 from .session import REUSE, RecapSession
+from .types import AttentionBranch, BlockSummary, ClosureBank
 
 __all__ = [
-    "EXACT", "REFRESH", "REUSE", "SPARSE", "Controller", "DetailBank", "HostBankOperator",
+    "EXACT", "REFRESH", "REUSE", "SPARSE", "AttentionBranch", "BlockSummary", "ClosureBank",
+    "Controller", "DetailBank", "HostBankOperator",
     "Layout", "OperatingPoint", "Operator", "OperatorConfig", "RecapConfig", "RecapSession",
     "SparseAttention", "SparseGeometry", "config_from_dict", "hilbert_permutation", "install",
     "load_config", "register_builder",

@@ -185,3 +185,29 @@ def test_operator_host_errors():
         op.attend(0, torch.zeros(1, 1, 128, 64, dtype=torch.bfloat16),
                   torch.zeros(1, 1, 128, 64, dtype=torch.bfloat16),
                   torch.zeros(1, 1, 128, 64, dtype=torch.bfloat16))
+
+
+def test_attention_branches_over_disjoint_keys_merge_to_the_full_softmax():
+    # AttentionBranch.merge: softmax over keys A and over keys B, merged in LSE space,
+    # equals the softmax over A and B together (closed form, fp64 reference).
+    from recap_amd import AttentionBranch
+
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(3, 17, 16, generator=g, dtype=torch.float64)
+    k = torch.randn(3, 40, 16, generator=g, dtype=torch.float64)
+    v = torch.randn(3, 40, 16, generator=g, dtype=torch.float64)
+    logits = q @ k.transpose(-1, -2) * 0.25
+
+    def branch(idx):
+        sub = logits[..., idx]
+        return AttentionBranch(torch.softmax(sub, -1) @ v[:, idx], torch.logsumexp(sub, -1))
+
+    a, b = branch(list(range(0, 40, 3))), branch([i for i in range(40) if i % 3])
+    full = branch(list(range(40)))
+    merged = a.merge(b)
+    torch.testing.assert_close(merged.output, full.output.float().double(), atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(merged.lse.double(), full.lse, atol=1e-5, rtol=1e-5)
+    # A branch with no keys (lse -inf) drops out.
+    empty = AttentionBranch(torch.zeros_like(a.output), torch.full_like(a.lse, float("-inf")))
+    same = a.merge(empty)
+    torch.testing.assert_close(same.output, a.output.float().double(), atol=1e-6, rtol=1e-6)
