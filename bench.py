@@ -68,6 +68,26 @@ def recorded_traffic(workload: str) -> float | None:
     return None
 
 
+def gemm_peak_tflops(n: int = 8192, reps: int = 10) -> float:
+    """Measured bf16 GEMM rate of the vendor library (torch.matmul -> hipBLASLt) on random
+    N(0,1) operands: the practical MFMA ceiling on this box (random data draws more power
+    than the published peak assumes)."""
+    import torch
+    g = torch.Generator(device="cuda").manual_seed(7)
+    a = torch.randn(n, n, device="cuda", dtype=torch.bfloat16, generator=g)
+    b = torch.randn(n, n, device="cuda", dtype=torch.bfloat16, generator=g)
+    for _ in range(3):
+        torch.matmul(a, b)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        torch.matmul(a, b)
+    e.record()
+    torch.cuda.synchronize()
+    return 2.0 * n ** 3 * reps / (s.elapsed_time(e) / 1e3) / 1e12
+
+
 def copy_calibration(reps: int = 5) -> int:
     """A plain device copy of COPY_CAL_BYTES, the known-size reference for the FETCH_SIZE /
     WRITE_SIZE counters: each dispatch reads and writes exactly COPY_CAL_BYTES."""
@@ -357,6 +377,11 @@ def main() -> int:
         dense_ms = s.elapsed_time(e) / args.dense_reps
         result["dense_sdpa_ms"] = round(dense_ms, 3)
         result["speedup_vs_dense_sdpa"] = round(dense_ms / ms, 2)
+        gemm = gemm_peak_tflops()
+        result["gemm_bf16_tflops_measured"] = round(gemm, 1)
+        result["roofline"]["frac_of_measured_gemm"] = round(
+            result["roofline"]["achieved"] / gemm, 4)
+        log(f"[bench] hipBLASLt bf16 GEMM 8192^3 (random operands): {gemm:.0f} TFLOP/s")
         log(f"[bench] dense SDPA {dense_ms:.2f} ms ({dense_tflop / dense_ms * 1e3:.0f} TFLOP/s)")
         if args.cpu_heads > 0:
             log("[bench] CPU baseline sample ...")
