@@ -13,6 +13,7 @@ from HIP events recorded on the same stream inside the timed calls.  Prints one 
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import math
 import os
@@ -279,6 +280,10 @@ def main() -> int:
     log(f"[bench] workload {wl.name}: heads={wl.heads} d={wl.dim} N={wl.tokens}")
     q0, k0, v0 = make_qkv(wl, seed=0, device=dev)
     q1, k1, v1 = (perturb(x, 0.02, seed=0, step=1) for x in (q0, k0, v0))
+    digest = hashlib.sha256()
+    for x in (q1, k1, v1):  # the timed calls' inputs, native [B, H, N, d] bf16 bytes
+        digest.update(x.contiguous().view(torch.uint16).cpu().numpy().tobytes())
+    input_sha256 = digest.hexdigest()
     layout = Layout.from_permutation(hilbert_permutation(wl.grid), text_tokens=wl.text_tokens,
                                      text_first=wl.text_first)
     op = Operator.build(OperatorConfig(head_density=wl.density), SparseGeometry.build(layout, 128),
@@ -346,6 +351,9 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic: N(0,1) + 3-D sinusoidal positional field on Q/K, seed 0, 2% drift "
                 "between the refresh and the timed sparse calls",
+        "generator": "recap_amd.synthetic.make_qkv(workload, seed=0) then "
+                     "perturb(x, 0.02, seed=0, step=1) for q, k, v",
+        "input_sha256": input_sha256,
         "config": {"workload": wl.name, "batch": 1, "heads": wl.heads, "head_dim": wl.dim,
                    "tokens": wl.tokens, "video_tokens": wl.video_tokens,
                    "text_tokens": wl.text_tokens, "block": 128, "density": wl.density},

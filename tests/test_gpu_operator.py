@@ -81,6 +81,32 @@ def test_refresh_sparse_sequence_vs_oracle(cuda, name):
     assert_close_bf16(out.cpu().float(), ref.last["out_f32"], f"sparse-3 {name}")
 
 
+@pytest.mark.parametrize("name,dtype,batch", [
+    ("text-first-ragged", torch.float16, 1),   # fp16 inputs (the boundary accepts both)
+    ("text-last-d128", torch.float16, 1),
+    ("text-first-ragged", torch.bfloat16, 2),  # CFG-batched calls, banks = B * H
+])
+def test_fp16_and_batched_calls_vs_oracle(cuda, name, dtype, batch):
+    wl = SMALL[name]
+    print(f"case {name} {dtype} batch={batch}", flush=True)
+    q, k, v = make_qkv(wl, seed=3, batch=batch, dtype=dtype)
+    op, perm = build(wl)
+    ref = O.OracleOperator(wl.grid, wl.text_tokens, wl.text_first, wl.density, permutation=perm)
+    g = lambda x: x.to(cuda)  # noqa: E731
+    op.begin_step(0, REFRESH)
+    out = op.attend(0, g(q), g(k), g(v))
+    assert out.dtype == dtype and out.shape == q.shape
+    ref.refresh(0, q, k, v, dtype=dtype)
+    assert_close_bf16(out.cpu().float(), ref.last["out_f32"], f"refresh {name} {dtype} b{batch}")
+    inject(ref, op, 0, wl)
+    q1, k1, v1 = (perturb(x, 0.02, seed=4, step=1) for x in (q, k, v))
+    op.begin_step(1, SPARSE)
+    out = op.attend(0, g(q1), g(k1), g(v1))
+    assert out.dtype == dtype
+    ref.sparse(0, q1, k1, v1, dtype=dtype)
+    assert_close_bf16(out.cpu().float(), ref.last["out_f32"], f"sparse {name} {dtype} b{batch}")
+
+
 @pytest.mark.parametrize("name", list(SMALL))
 def test_sparse_vs_oracle_with_independent_state(cuda, name):
     """End to end with separately computed refinement states.  The coarse tail's gate
