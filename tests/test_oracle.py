@@ -390,6 +390,86 @@ def test_refresh_then_sparse_reproduces_dense_cpu_config():
     assert (err[:, perm[:rows]] <= bound + 2e-6).all()
     assert zeroed.any() and (~zeroed).any()
     assert err.median() < 1e-5
-    # with the BASELINE's fixed drift weight of 0.8 the output moves toward head (+) coarse
+    # with a fixed drift weight of 0.8 the output moves toward head (+) coarse
     partial = op.sparse(0, q, k, v, dtype=torch.float32, alpha_override=0.8)
     assert (partial - dense).abs().max() > (sparse - dense).abs().max()
+
+
+# -- functions pinned by closed forms and published shapes --------------------------------
+
+
+@pytest.mark.parametrize("n_video,n_tokens,expect", [
+    # (nb, last block, tb, ds, rows) of the four reference configurations
+    (4096, 4096, (32, 128, 32, 32, 4096)),
+    (32760, 32760, (256, 120, 256, 256, 32640)),
+    (44880, 45106, (351, 80, 353, 350, 44800)),
+    (118800, 119056, (929, 16, 931, 928, 118784)),
+])
+def test_block_geometry_matches_the_reference_shapes(n_video, n_tokens, expect):
+    geo = O.block_geometry(n_video, n_tokens)
+    nb, last, tb, ds, rows = expect
+    assert (geo["nb"], geo["tb"], geo["ds"], geo["rows"]) == (nb, tb, ds, rows)
+    assert geo["counts"][-1] == last and float(geo["counts"].sum()) == n_video
+
+
+def test_closure_basis_diagonalises_the_symmetrised_scatter():
+    g = torch.Generator().manual_seed(11)
+    a = torch.randn(2, 16, 16, generator=g)
+    spd = a @ a.transpose(-1, -2) + 0.1 * torch.eye(16)
+    skew = torch.randn(2, 16, 16, generator=g)
+    skew = skew - skew.transpose(-1, -2)
+    u = O.closure_basis(spd + skew).double()  # the antisymmetric part must not matter
+    eye = torch.eye(16, dtype=torch.float64)
+    torch.testing.assert_close(u.transpose(-1, -2) @ u, eye.expand(2, 16, 16), atol=1e-5, rtol=0)
+    rot = u.transpose(-1, -2) @ spd.double() @ u
+    off = rot - torch.diag_embed(torch.diagonal(rot, dim1=-2, dim2=-1))
+    assert float(off.abs().max()) < 1e-4 * float(rot.abs().max())
+
+
+def test_split_hi_lo_is_two_bf16_terms_of_the_value():
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(4096, generator=g) * torch.logspace(-6, 6, 4096)
+    hi, lo = O.split_hi_lo(x)
+    assert torch.equal(hi, hi.to(torch.bfloat16).float())
+    assert torch.equal(lo, lo.to(torch.bfloat16).float())
+    assert torch.equal(hi, x.to(torch.bfloat16).float())
+    # bf16 keeps 8 significant bits: |x - hi| <= 2^-9 |x|, |x - hi - lo| <= 2^-9 |x - hi|
+    err = (x.double() - hi.double() - lo.double()).abs()
+    assert bool((err <= 2.0 ** -17 * x.double().abs()).all())
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_rotated_query_square_and_value_drift_closed_forms(dtype):
+    g = torch.Generator().manual_seed(13)
+    q = torch.randn(2, 40, 32, generator=g).to(dtype)
+    u = torch.linalg.qr(torch.randn(2, 32, 32, generator=g))[0]
+    c = torch.randn(2, 32, 32, generator=g) * 0.1
+    qsq = O.rotated_query_square(q, u, dtype)
+    drift = O.value_drift(q, c, 0.125, dtype)
+    # values rounded to the query type (held in fp32)
+    assert torch.equal(qsq.float(), qsq.to(dtype).float())
+    assert torch.equal(drift.float(), drift.to(dtype).float())
+    # fp64 values of (U^T q)^2 and s C q per row, from the dtype-rounded operands
+    rot = q.double() @ u.to(dtype).double()
+    want_sq = rot.to(dtype).double() ** 2
+    want_drift = (q.double() @ c.to(dtype).double().transpose(-1, -2)).to(dtype).double() * 0.125
+    ulp = 2.0 ** -23 if dtype == torch.float32 else 2.0 ** -8
+    torch.testing.assert_close(qsq.double(), want_sq, rtol=4 * ulp, atol=1e-12)
+    torch.testing.assert_close(drift.double(), want_drift, rtol=4 * ulp, atol=1e-12)
+
+
+def test_drift_center_is_the_mean_row_shift():
+    gl = torch.tensor([[1.0, 2.0, 3.0], [0.0, 0.0, 0.0]])
+    glref = torch.tensor([[0.0, 1.0, 1.0], [1.0, 1.0, 1.0]])
+    torch.testing.assert_close(O.drift_center(gl, glref), torch.tensor([4.0 / 3.0, -1.0]))
+
+
+def test_topk_margin_brute_force():
+    g = torch.Generator().manual_seed(14)
+    s = torch.randn(3, 7, 20, generator=g)
+    gaps = []
+    for row in s.reshape(-1, 20):
+        top = sorted(row.tolist(), reverse=True)
+        gaps.append(top[4] - top[5])
+    assert O.topk_margin(s, 5) == pytest.approx(min(gaps), abs=1e-6)
+    assert O.topk_margin(s, 20) == float("inf")
