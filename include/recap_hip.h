@@ -60,6 +60,23 @@ int recap_kv_pack(const void* k, const void* v, int dtype, int64_t batch, int64_
                   const int32_t* rowmap, int64_t n_tokens, int64_t n_video, void* k_tiles,
                   void* vt_tiles, float* k_means, float* v_means, void* stream);
 
+/* Stage 1 in one call: pooled query means, fp32 block scores against k_means (from
+ * recap_kv_pack), the top-keep selection with keep = max(1, round(density * nb)) (round half
+ * to even) and the partial last block forced, then the kernel block mask.  partition
+ * [banks, nb, nb] and kernel_mask [banks, tb, tb] (bool bytes); the intermediates live in
+ * `workspace` (16-byte aligned, recap_pool_select_workspace_size bytes).  The kernel mask
+ * replaces a CSR block list: the attention kernel compacts each mask row on chip.
+ * Replaces SparseAttention.head_partition + block_proxy_mask + build_kernel_block_mask
+ * (recap/sparse/attention.py:74-94, recap/sparse/router.py:10-23,
+ * recap/kernels/block_sparse.py:52-75). */
+int64_t recap_pool_select_workspace_size(int64_t banks, int64_t n_blocks, int64_t dim);
+int recap_pool_select(const void* q, int dtype, int64_t batch, int64_t heads, int64_t dim,
+                      int64_t stride_b, int64_t stride_h, int64_t stride_n,
+                      const int32_t* rowmap, int64_t n_tokens, int64_t n_video,
+                      const float* k_means, float scale, double density, void* workspace,
+                      int64_t workspace_bytes, uint8_t* partition, uint8_t* kernel_mask,
+                      void* stream);
+
 /* fp32 block scores [banks, nb, nb] = fp32(scale) * (qbar . kbar), fixed summation order.
  * Replaces the matmul + mul_ of block_proxy_mask, recap/sparse/router.py:18-19. */
 int recap_block_scores(const float* q_means, const float* k_means, int64_t banks,

@@ -29,6 +29,9 @@ SIGNATURES: dict[str, tuple] = {
     "recap_kv_pack": (_I, [_P, _P, _I, _I64, _I64, _I64, *_STRIDES, *_STRIDES, _P, _I64, _I64,
                            _P, _P, _P, _P, _P]),
     "recap_block_scores": (_I, [_P, _P, _I64, _I64, _I64, _F, _P, _P]),
+    "recap_pool_select_workspace_size": (_I64, [_I64, _I64, _I64]),
+    "recap_pool_select": (_I, [_P, _I, _I64, _I64, _I64, *_STRIDES, _P, _I64, _I64, _P, _F,
+                               ctypes.c_double, _P, _I64, _P, _P, _P]),
     "recap_topk_blocks": (_I, [_P, _I64, _I64, _I64, _I, _P, _P]),
     "recap_kernel_block_mask": (_I, [_P, _I64, _I64, _I64, _P, _P]),
     "recap_mask_overlap": (_I, [_P, _P, _I64, _P, _P]),

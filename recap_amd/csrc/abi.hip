@@ -8,6 +8,8 @@
 #include <vector>
 
 #include "../../include/recap_hip.h"
+
+#include <cmath>
 #include "kernels.hpp"
 
 using namespace recap;
@@ -213,6 +215,43 @@ int recap_kernel_block_mask(const uint8_t* partition, int64_t banks, int64_t n_t
   const Geom g = geometry(n_tokens, n_video);
   KmaskArgs a{partition, (int)banks, (int)g.nb, (int)g.tb, (int)g.ds, kernel_mask};
   return hip_status(run_kernel_mask(a, as_stream(stream)), "kernel_mask launch");
+}
+
+static int64_t align256(int64_t bytes) { return (bytes + 255) / 256 * 256; }
+
+int64_t recap_pool_select_workspace_size(int64_t banks, int64_t n_blocks, int64_t dim) {
+  if (banks < 1 || n_blocks < 1 || dim < 1) return -1;
+  return align256(banks * n_blocks * dim * 4) + align256(banks * n_blocks * n_blocks * 4);
+}
+
+int recap_pool_select(const void* q, int dtype, int64_t batch, int64_t heads, int64_t dim,
+                      int64_t stride_b, int64_t stride_h, int64_t stride_n,
+                      const int32_t* rowmap, int64_t n_tokens, int64_t n_video,
+                      const float* k_means, float scale, double density, void* workspace,
+                      int64_t workspace_bytes, uint8_t* partition, uint8_t* kernel_mask,
+                      void* stream) {
+  CHECK(check_tokens(n_tokens, n_video));
+  REQUIRE(k_means && workspace && partition && kernel_mask, "NULL pointer");
+  REQUIRE(density > 0.0 && density < 1.0, "density %g outside (0, 1)", density);
+  REQUIRE(batch >= 1 && heads >= 1, "bad batch/heads");
+  const Geom g = geometry(n_tokens, n_video);
+  const int64_t banks = batch * heads;
+  const int64_t need = recap_pool_select_workspace_size(banks, g.nb, dim);
+  REQUIRE(need > 0 && workspace_bytes >= need, "workspace of %lld bytes, need %lld",
+          (long long)workspace_bytes, (long long)need);
+  REQUIRE(aligned16(workspace), "workspace must be 16-byte aligned");
+  // keep = max(1, round(density * nb)), Python's round-half-even (recap/sparse/attention.py:84)
+  int64_t keep = (int64_t)std::nearbyint(density * (double)g.nb);
+  keep = keep < 1 ? 1 : (keep > g.nb ? g.nb : keep);
+  float* q_means = static_cast<float*>(workspace);
+  float* scores = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                           align256(banks * g.nb * dim * 4));
+  CHECK(recap_pool_blocks(q, dtype, batch, heads, dim, stride_b, stride_h, stride_n, rowmap,
+                          n_tokens, n_video, q_means, stream));
+  CHECK(recap_block_scores(q_means, k_means, banks, g.nb, dim, scale, scores, stream));
+  CHECK(recap_topk_blocks(scores, banks, g.nb, keep, n_video % kBlock != 0 ? 1 : 0, partition,
+                          stream));
+  return recap_kernel_block_mask(partition, banks, n_tokens, n_video, kernel_mask, stream);
 }
 
 int recap_mask_overlap(const uint8_t* new_mask, const uint8_t* old_mask, int64_t count,

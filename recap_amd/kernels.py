@@ -169,6 +169,22 @@ def mask_overlap(new: torch.Tensor, old: torch.Tensor) -> tuple[int, int]:
     return int(kept), int(total)
 
 
+def pool_select(q: torch.Tensor, k_means: torch.Tensor, rowmap: torch.Tensor, geo: Geometry,
+                density: float, scale: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """Stage 1 in one library call: (partition [banks, nb, nb], kernel mask [banks, tb, tb])."""
+    b, h, n, d = q.shape
+    banks = b * h
+    k_means = k_means.contiguous()
+    size = int(_lib.load().recap_pool_select_workspace_size(banks, geo.nb, d))
+    work = torch.empty(size, dtype=torch.uint8, device=q.device)
+    part = torch.empty(banks, geo.nb, geo.nb, dtype=torch.bool, device=q.device)
+    kmask = torch.empty(banks, geo.tb, geo.tb, dtype=torch.bool, device=q.device)
+    call("recap_pool_select", *_qkv_args(q), rowmap.data_ptr(), n, geo.n_video,
+         k_means.data_ptr(), float(scale), float(density), work.data_ptr(), size,
+         part.data_ptr(), kmask.data_ptr(), _stream())
+    return part, kmask
+
+
 def select_blocks(q: torch.Tensor, k_means: torch.Tensor, rowmap: torch.Tensor, geo: Geometry,
                   density: float, scale: float) -> torch.Tensor:
     """Partition ``[banks, nb, nb]`` bool (recap/sparse/attention.py:74-94)."""

@@ -328,9 +328,11 @@ class Operator:
     # -- refresh -------------------------------------------------------------------------
 
     def _select(self, layer, q, kv, geo, rowmap):
+        """Partition and kernel mask in one library call (recap/operator.py:353-361)."""
         b, h = q.shape[:2]
-        part = layer.head_partition(q, kv, rowmap, geo, K.scale_for(q.shape[-1]))
-        return part.reshape(b, h, geo.nb, geo.nb), K.kernel_block_mask(part, geo)
+        part, kmask = K.pool_select(q, kv.k_means, rowmap, geo, layer.config.head_density,
+                                    K.scale_for(q.shape[-1]))
+        return part.reshape(b, h, geo.nb, geo.nb), kmask
 
     @torch.no_grad()
     def _refresh(self, layer, bank, q, kv, geo, rowmap, full_output, full_lse) -> None:

@@ -59,6 +59,9 @@ def test_stage1_pool_scores_masks_bit_exact(cuda, name, heads):
     assert torch.equal(part.cpu(), part_ref)
     kmask = K.kernel_block_mask(part, geo)
     assert torch.equal(kmask.cpu(), O.kernel_block_mask(part_ref, wl.tokens, wl.video_tokens))
+    # the one-call stage 1 gives the same partition and kernel mask
+    part1, kmask1 = K.pool_select(qg, kv.k_means, rowmap, geo, wl.density, scale)
+    assert torch.equal(part1, part) and torch.equal(kmask1, kmask)
 
 
 @pytest.mark.parametrize("name", list(SMALL))

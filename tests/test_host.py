@@ -69,6 +69,14 @@ def test_argument_validation_before_launch():
     with pytest.raises(ValueError, match="kernel blocks"):
         _lib.call("recap_dense_attn", 16, _lib.RECAP_BF16, 1, 1, 64, 0, 0, 64, 16, 16, 16,
                   2049 * 128, 0.125, 16, 0, 0, 64, 16, None)
+    need = _lib.load().recap_pool_select_workspace_size(2, 4, 64)
+    assert need == 2048 + 256  # 2*4*64 fp32 means, then 2*4*4 fp32 scores, 256-byte aligned
+    with pytest.raises(ValueError, match="workspace"):
+        _lib.call("recap_pool_select", 16, _lib.RECAP_BF16, 1, 2, 64, 0, 0, 64, 16, 512, 512,
+                  16, 0.125, 0.25, 16, need - 1, 16, 16, None)
+    with pytest.raises(ValueError, match="density"):
+        _lib.call("recap_pool_select", 16, _lib.RECAP_BF16, 1, 2, 64, 0, 0, 64, 16, 512, 512,
+                  16, 0.125, 1.5, 16, need, 16, 16, None)
 
 
 def test_workspace_queries():
