@@ -32,15 +32,10 @@ constexpr int kMaxTiles = 2048;
 // stays below 2^8, exact in fp32 and bf16, and the O rescale is skipped.
 constexpr float kRescaleSlack = 8.0f;
 
-typedef __attribute__((address_space(3))) void lds_void;
-
 // s_waitcnt immediate (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
 // that waits for all vector memory operations of this wave -- the tile copies into LDS --
 // and all its LDS reads.
 constexpr int kWaitVmLgkm0 = 0x7 << 4;
-
-// Word 3 of a raw buffer resource on CDNA (32-bit data format, no swizzle).
-constexpr int kBufferRsrcWord3 = 0x00020000;
 
 // Wait for this wave's copies into LDS and its LDS reads, then for every wave of the
 // workgroup: afterwards the copied sub-tiles are visible and the slots read so far may be
@@ -53,7 +48,9 @@ __device__ inline void tile_barrier() {
 }
 
 // Each wave owns kGroups groups of 32 query rows, so every K/V fragment it reads from LDS
-// feeds kGroups MFMAs; a 128-row query block then takes kThreads threads.
+// feeds kGroups MFMAs; a 128-row query block then takes kThreads threads.  kGroups = 2
+// halves the LDS reads and is correct, but at d = 128 it needs one wave per SIMD and the
+// compiler then keeps every MFMA result in AGPRs: it measured slower.
 constexpr int kGroups = 1;
 constexpr int kRowsPerWave = 32 * kGroups;
 constexpr int kThreads = 64 * (kBlock / kRowsPerWave);

@@ -23,8 +23,6 @@ namespace recap {
 
 constexpr int kMaxVideoBlocks = 4096;
 
-typedef __attribute__((address_space(3))) void lds_void;
-constexpr int kBufferRsrcWord3 = 0x00020000;  // raw buffer resource word 3 on CDNA
 constexpr float kTailSlack = 8.0f * kLn2;      // lazy-max slack, natural-log units
 
 template <class T, int D>

@@ -157,6 +157,12 @@ struct TileGeom {
   }
 };
 
+// LDS address space, for the buffer-load-to-LDS builtin's destination.
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Word 3 of a raw buffer resource on CDNA (32-bit data format, no swizzle).
+constexpr int kBufferRsrcWord3 = 0x00020000;
+
 // Coarse-tail table tiles: 32 key blocks (slots) per tile.  K-bar and w tiles are K-tile
 // rows (TileGeom<D>::k_off with the slot as the row); the V-bar tile is transposed,
 // [D][32 positions] with 64-byte rows, position p holding slot swap23(p), and 16-byte chunks
