@@ -123,6 +123,14 @@ int recap_closure_stats(const void* k_tiles, const void* vt_tiles, const float* 
 int recap_partial_reduce(const float* partial, int64_t banks, int64_t groups, int64_t elems,
                          float divisor, float* out, void* stream);
 
+/* Eigenvalues (ascending, [batch, n]) and orthonormal eigenvectors (columns, [batch, n, n])
+ * of the symmetrised 0.5 (a + a^T) of `batch` row-major fp32 n x n matrices, n <= 128:
+ * the contract of torch.linalg.eigh.  Two-sided parallel Jacobi in one workgroup per matrix;
+ * eigenvectors are unique up to sign (and to a rotation within a repeated eigenvalue).
+ * Replaces the torch.linalg.eigh call of closure_basis, recap/sparse/closure.py:75-81. */
+int recap_symmetric_eigen(const float* a, int64_t batch, int64_t n, float* eigenvalues,
+                          float* eigenvectors, void* stream);
+
 /* Query-type tables of the coarse tail: w = fold_rank(variance, rank) (columns in swap23
  * order), kbar, vbar, each written as tile images of 32 key blocks, [banks, ceil(nb/32)*32,
  * dim] elements (rows past nb zero): kbar and w tiles in the packed K-tile layout, vbar

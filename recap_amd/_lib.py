@@ -39,6 +39,7 @@ SIGNATURES: dict[str, tuple] = {
     "recap_closure_stats": (_I, [_P, _P, _P, _I, _P, _P, _I64, _I64, _I64, _I64, _I64, _I, _P,
                                  _P, _P, _P]),
     "recap_partial_reduce": (_I, [_P, _I64, _I64, _I64, _F, _P, _P]),
+    "recap_symmetric_eigen": (_I, [_P, _I64, _I64, _P, _P, _P]),
     "recap_coarse_tables": (_I, [_P, _P, _P, _I, _I64, _I64, _I64, _I64, _P, _P, _P, _P]),
     "recap_basis_tables": (_I, [_P, _P, _I, _I64, _I64, _P, _P, _P, _P, _P]),
     "recap_coarse_tail": (_I, [_P, _I, _I64, _I64, _I64, *_STRIDES, _P, _P, _P, _P, _P, _P, _P,

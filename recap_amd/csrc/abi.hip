@@ -304,6 +304,17 @@ int recap_partial_reduce(const float* partial, int64_t banks, int64_t groups, in
                     "partial_reduce launch");
 }
 
+int recap_symmetric_eigen(const float* a, int64_t batch, int64_t n, float* eigenvalues,
+                          float* eigenvectors, void* stream) {
+  REQUIRE(a && eigenvalues && eigenvectors, "NULL pointer");
+  REQUIRE(batch >= 1 && batch <= 65535, "bad batch %lld", (long long)batch);
+  REQUIRE(n >= 1 && n <= 128, "matrix order %lld outside [1, 128]", (long long)n);
+  EigenArgs e{};
+  e.a = a; e.batch = (int)batch; e.n = (int)n; e.m = (int)(n + (n & 1));
+  e.max_sweeps = 40; e.values = eigenvalues; e.vectors = eigenvectors;
+  return hip_status(run_symmetric_eigen(e, as_stream(stream)), "symmetric_eigen launch");
+}
+
 int recap_coarse_tables(const float* variance, const float* k_means, const float* v_means,
                         int dtype, int64_t banks, int64_t n_blocks, int64_t dim, int64_t rank,
                         void* w, void* kbar, void* vbar, void* stream) {

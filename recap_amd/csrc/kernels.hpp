@@ -57,6 +57,13 @@ struct BasisArgs {
 };
 hipError_t run_basis_tables(const BasisArgs& a, int dtype, hipStream_t s);
 
+// Symmetric eigen-decomposition of the closure scatter (eigen.hip).
+struct EigenArgs {
+  const float* a; int batch, n, m, max_sweeps;   // m = n rounded up to even
+  float* values; float* vectors;                 // [batch][n], [batch][n][n] (columns)
+};
+hipError_t run_symmetric_eigen(const EigenArgs& a, hipStream_t s);
+
 // Coarse tail (coarse.hip).
 struct CoarseArgs {
   const uint16_t* q; int64_t sB, sH, sN;

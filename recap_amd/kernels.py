@@ -233,6 +233,21 @@ def partial_reduce(part: torch.Tensor, divisor: float) -> torch.Tensor:
     return out
 
 
+def symmetric_eigen(a: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(eigenvalues ascending ``[..., n]``, eigenvectors as columns ``[..., n, n]``) of the
+    symmetrised fp32 ``0.5 (a + a^T)``, n <= 128: the contract of ``torch.linalg.eigh``
+    that closure_basis relies on (recap/sparse/closure.py:75-81)."""
+    if a.dim() < 2 or a.shape[-1] != a.shape[-2]:
+        raise ValueError(f"symmetric_eigen needs square matrices, got {tuple(a.shape)}")
+    n = a.shape[-1]
+    flat = a.reshape(-1, n, n).to(torch.float32).contiguous()
+    values = torch.empty(flat.shape[0], n, dtype=torch.float32, device=a.device)
+    vectors = torch.empty_like(flat)
+    call("recap_symmetric_eigen", flat.data_ptr(), flat.shape[0], n, values.data_ptr(),
+         vectors.data_ptr(), _stream())
+    return values.reshape(a.shape[:-1]), vectors.reshape(a.shape)
+
+
 @dataclass
 class BasisTables:
     u_hi_t: torch.Tensor | None = None

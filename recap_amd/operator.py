@@ -63,8 +63,7 @@ class SparseAttention:
         dtype = kv.dtype
         if self._basis is None:
             _, cvk, scatter = K.closure_stats(kv, geo, _lib.CLOSURE_CVK | _lib.CLOSURE_SCATTER)
-            symmetric = 0.5 * (scatter + scatter.transpose(-1, -2))
-            basis = torch.linalg.eigh(symmetric)[1].contiguous()
+            basis = K.symmetric_eigen(scatter)[1]   # symmetrises 0.5 (S + S^T) itself
             split = K.basis_tables(basis, None, dtype, split=True)
             var, _, _ = K.closure_stats(kv, geo, _lib.CLOSURE_ROT, split.u_hi_t, split.u_lo_t)
             # Order the basis by pooled within-block variance (recap/sparse/attention.py:137-152).

@@ -69,6 +69,10 @@ def test_argument_validation_before_launch():
     with pytest.raises(ValueError, match="kernel blocks"):
         _lib.call("recap_dense_attn", 16, _lib.RECAP_BF16, 1, 1, 64, 0, 0, 64, 16, 16, 16,
                   2049 * 128, 0.125, 16, 0, 0, 64, 16, None)
+    with pytest.raises(ValueError, match="matrix order"):
+        _lib.call("recap_symmetric_eigen", 16, 2, 129, 16, 16, None)
+    with pytest.raises(ValueError, match="matrix order"):
+        _lib.call("recap_symmetric_eigen", 16, 2, 0, 16, 16, None)
     need = _lib.load().recap_pool_select_workspace_size(2, 4, 64)
     assert need == 2048 + 256  # 2*4*64 fp32 means, then 2*4*4 fp32 scores, 256-byte aligned
     with pytest.raises(ValueError, match="workspace"):
