@@ -156,8 +156,14 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
   constexpr int NDT = D / 32;                 // 32-row tiles of O^T
   constexpr int HALF = G::kHalfBytes;         // K or V^T image of a 64-key sub-tile
   constexpr int NDMA = HALF / (16 * kThreads);  // 16-byte copies per thread per image
-  // LDS: K images of sub-tiles 2k / 2k+1 in slots 0 / 1, V^T images likewise after them.
-  __shared__ __attribute__((aligned(16))) char lds[4 * HALF];
+  // LDS: K images of sub-tiles 2k / 2k+1 in k_lds0 / k_lds1, V^T images likewise.  Four
+  // separate arrays, each access naming one of them at compile time (the step parity is
+  // static): the compiler can then tell that a step's fragment reads do not touch the slots
+  // its copies are filling, and does not wait for those copies before the reads.
+  __shared__ __attribute__((aligned(16))) char k_lds0[HALF];
+  __shared__ __attribute__((aligned(16))) char k_lds1[HALF];
+  __shared__ __attribute__((aligned(16))) char v_lds0[HALF];
+  __shared__ __attribute__((aligned(16))) char v_lds1[HALF];
   __shared__ int list[MODE == kModeDense ? 1 : kMaxTiles];
   __shared__ int scan[kThreads];
 
@@ -217,8 +223,6 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
           rs, (lds_void*)(dst + 16 * kThreads * i + 1024 * wave), 16,
           16 * kThreads * i + 16 * t, off, 0, 0);
   };
-  char* const kslot = lds;
-  char* const vslot = lds + 2 * HALF;
 
   // Query group q of this wave: rows 32 q .. 32 q + 31 of the wave's kRowsPerWave.
   int row[kGroups], nat[kGroups];
@@ -230,10 +234,10 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
     nat[q] = valid[q] ? a.rowmap[row[q]] : 0;
   }
   if (nsub > 0) {
-    copy(krs, image(0), kslot);
-    copy(vrs, image(0), vslot);
+    copy(krs, image(0), k_lds0);
+    copy(vrs, image(0), v_lds0);
   }
-  if (nsub > 1) copy(krs, image(1), kslot + HALF);
+  if (nsub > 1) copy(krs, image(1), k_lds1);
   u32x4 qreg[kGroups][NS];
 #pragma unroll
   for (int q = 0; q < kGroups; ++q) {
@@ -312,14 +316,16 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
   // work: while S_{it+1} runs, pairs of P_it = exp2(S_it scale log2e - m) values (two exp,
   // packed for the PV MFMAs); while PV_it runs, the row max over pairs of S_{it+1} scores.
   // The matrix core then works while the VALU does, instead of one after the other.
+  // `it` is even at every call with parity tag 0 and odd with tag 1.
   auto step = [&](int it, f32x16 (&cur)[kGroups][2], f32x16 (&nxt)[kGroups][2], auto mask_tag,
-                  auto next_tag) {
+                  auto next_tag, auto parity_tag) {
     constexpr bool kNext = decltype(next_tag)::value;
     constexpr bool kMask = decltype(mask_tag)::value;
-    if (it + 1 < nsub) copy(vrs, image(it + 1), vslot + ((it + 1) & 1) * HALF);
-    if (it + 2 < nsub) copy(krs, image(it + 2), kslot + (it & 1) * HALF);
-    const char* kl = kslot + ((it + 1) & 1) * HALF;
-    const char* vl = vslot + (it & 1) * HALF;
+    constexpr bool kOdd = decltype(parity_tag)::value;
+    if (it + 1 < nsub) copy(vrs, image(it + 1), kOdd ? v_lds0 : v_lds1);
+    if (it + 2 < nsub) copy(krs, image(it + 2), kOdd ? k_lds1 : k_lds0);
+    const char* kl = kOdd ? k_lds0 : k_lds1;   // K_{it+1}
+    const char* vl = kOdd ? v_lds1 : v_lds0;   // V_it
     constexpr int NQK = kNext ? 2 * NS : 0;  // S fragments of this step
     constexpr int NPV = 4 * NDT;             // PV fragments
     constexpr int NN = NQK + NPV;
@@ -401,7 +407,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
   const int plain = ragged_last ? nsub - 2 : nsub;  // sub-tiles below this need no mask
   f32x16 sa[kGroups][2], sb[kGroups][2];
   if (nsub > 0) {
-    qk(kslot, sa);
+    qk(k_lds0, sa);
     if (plain == 0) mask_tail(sa, 0);
     row_max(sa);
     tile_barrier();  // step 0 overwrites K slot 0 (read just now)
@@ -414,17 +420,18 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
   // no next sub-tile.
   int it = 0;
   for (; it + 4 < nsub; it += 2) {
-    step(it, sa, sb, F{}, Tr{});
-    step(it + 1, sb, sa, F{}, Tr{});
+    step(it, sa, sb, F{}, Tr{}, F{});
+    step(it + 1, sb, sa, F{}, Tr{}, Tr{});
   }
   if (nsub >= 4) {
-    step(it, sa, sb, F{}, Tr{});
-    if (ragged_last) step(it + 1, sb, sa, Tr{}, Tr{}); else step(it + 1, sb, sa, F{}, Tr{});
+    step(it, sa, sb, F{}, Tr{}, F{});
+    if (ragged_last) step(it + 1, sb, sa, Tr{}, Tr{}, Tr{});
+    else step(it + 1, sb, sa, F{}, Tr{}, Tr{});
     it += 2;
   }
   if (nsub >= 2) {
-    if (ragged_last) step(it, sa, sb, Tr{}, Tr{}); else step(it, sa, sb, F{}, Tr{});
-    step(it + 1, sb, sa, F{}, F{});
+    if (ragged_last) step(it, sa, sb, Tr{}, Tr{}, F{}); else step(it, sa, sb, F{}, Tr{}, F{});
+    step(it + 1, sb, sa, F{}, F{}, Tr{});
   }
 
 #pragma unroll
