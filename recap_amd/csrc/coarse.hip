@@ -33,9 +33,15 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
   constexpr int kMatBytes = D * D * 2;
   constexpr int kTabBytes = kCoarseSlots * D * 2;  // one table tile image
   constexpr int kStage = 3 * kTabBytes;            // the kbar, w, vbar tiles of one tile
-  constexpr int kBuf = kMatBytes > 2 * kStage ? kMatBytes : 2 * kStage;
   constexpr int NDMA = kTabBytes / 4096;           // 16-byte copies per thread per image
-  __shared__ __attribute__((aligned(16))) char buf[kBuf];
+  static_assert(2 * kStage >= kMatBytes, "a staged D x D matrix spans both stages");
+  // Two tile stages in separate arrays, each access naming one of them at compile time: the
+  // compiler can then tell that reads of one stage do not touch the copies filling the other,
+  // and does not wait for those copies first.  A staged D x D matrix (U^T, C_vk) keeps rows
+  // 0 .. D/2-1 in stage 0 and the rest in stage 1 (same swizzle: it depends on the row's low
+  // bits only).
+  __shared__ __attribute__((aligned(16))) char st0[kStage];
+  __shared__ __attribute__((aligned(16))) char st1[kStage];
   __shared__ unsigned omit[kMaxVideoBlocks / kCoarseSlots];
   __shared__ float wsum[4];
 
@@ -58,15 +64,22 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
     }
   }
 
-  // Stage U^T (query type, [D][D]) into LDS.
-  {
-    const uint16_t* us = a.u_t + (int64_t)bank * D * D;
-    for (int cc = t; cc < D * NCH; cc += 256) {
+  // Stage a D x D matrix of the query type (rows of 8-element chunks) into LDS.
+  auto stage_matrix = [&](const uint16_t* src) {
+    for (int cc = t; cc < D * NCH / 2; cc += 256) {
       const int row = cc / NCH, c = cc % NCH;
-      *reinterpret_cast<u32x4*>(buf + G::k_off(row, c)) =
-          *reinterpret_cast<const u32x4*>(us + row * D + c * 8);
+      *reinterpret_cast<u32x4*>(st0 + G::k_off(row, c)) =
+          *reinterpret_cast<const u32x4*>(src + row * D + c * 8);
+      *reinterpret_cast<u32x4*>(st1 + G::k_off(row, c)) =
+          *reinterpret_cast<const u32x4*>(src + (row + D / 2) * D + c * 8);
     }
-  }
+  };
+  // Fragment of row tile `rt` (32 rows) of a staged matrix; rt is a compile-time index.
+  auto matrix_frag = [&](int rt, int chunk) {
+    return rt < NDT / 2 ? lds_load16(st0, G::k_off(32 * rt + l32, chunk))
+                        : lds_load16(st1, G::k_off(32 * (rt - NDT / 2) + l32, chunk));
+  };
+  stage_matrix(a.u_t + (int64_t)bank * D * D);  // U^T
 
   const int r = qt * kBlock + wave * 32 + l32;  // always < rows
   const int nat = a.rowmap[r];
@@ -85,7 +98,7 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
     f32x16 acc = f32x16{};
 #pragma unroll
     for (int s = 0; s < NS; ++s)
-      acc = T::mfma32(lds_load16(buf, G::k_off(32 * ot + l32, 2 * s + g)), qreg[s], acc);
+      acc = T::mfma32(matrix_frag(ot, 2 * s + g), qreg[s], acc);
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       unsigned w[4];
@@ -118,8 +131,7 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
       __builtin_amdgcn_make_buffer_rsrc((void*)(a.w + tab_elems), 0, bank_tab, kBufferRsrcWord3);
   const __amdgpu_buffer_rsrc_t vrs =
       __builtin_amdgcn_make_buffer_rsrc((void*)(a.vbar + tab_elems), 0, bank_tab, kBufferRsrcWord3);
-  auto copy_tile = [&](int k, int stage) {
-    char* dst = buf + stage * kStage;
+  auto copy_tile = [&](int k, char* dst) {
     const int off = __builtin_amdgcn_readfirstlane(k * kTabBytes);
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) {
@@ -140,18 +152,17 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) oacc[dt] = f32x16{};
 
-  int k = next_tile(-1), stage = 0;
-  if (k < ntiles) copy_tile(k, 0);
-  while (k < ntiles) {
+  // Tile k from stage `cur` while the next tile is copied into stage `nxt`.
+  auto tile = [&](int k, const char* cur, char* nxt) {
     // This wave's copies of tile k have landed and every wave is done with the other stage.
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(0x7 << 4);  // vmcnt(0) lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     const int kn = next_tile(k);
-    if (kn < ntiles) copy_tile(kn, stage ^ 1);
+    if (kn < ntiles) copy_tile(kn, nxt);
 
-    const char* kb_lds = buf + stage * kStage;
+    const char* kb_lds = cur;
     const char* w_lds = kb_lds + kTabBytes;
     const char* vt_lds = kb_lds + 2 * kTabBytes;
     f32x16 sacc = f32x16{}, wacc = f32x16{};
@@ -217,20 +228,19 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
       for (int hh = 0; hh < 2; ++hh)
         oacc[dt] = T::mfma32(lds_load16(vt_lds, coarse_vt_off(d, 8 * (2 * hh + g))), pk[hh], oacc[dt]);
     }
-    k = kn;
-    stage ^= 1;
+    return kn;
+  };
+  int k = next_tile(-1);
+  if (k < ntiles) copy_tile(k, st0);
+  while (k < ntiles) {
+    k = tile(k, st0, st1);
+    if (k >= ntiles) break;
+    k = tile(k, st1, st0);
   }
 
   // Value drift s C_vk q in the output layout: stage C_vk over the tables' LDS.
   __syncthreads();
-  {
-    const uint16_t* cs = a.cvk + (int64_t)bank * D * D;
-    for (int cc = t; cc < D * NCH; cc += 256) {
-      const int row = cc / NCH, c = cc % NCH;
-      *reinterpret_cast<u32x4*>(buf + G::k_off(row, c)) =
-          *reinterpret_cast<const u32x4*>(cs + row * D + c * 8);
-    }
-  }
+  stage_matrix(a.cvk + (int64_t)bank * D * D);
   __syncthreads();
 
   const float l = pair_sum(lsum);
@@ -245,7 +255,7 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
     f32x16 dacc = f32x16{};
 #pragma unroll
     for (int s = 0; s < NS; ++s)
-      dacc = T::mfma32(lds_load16(buf, G::k_off(32 * dt + l32, 2 * s + g)), qreg[s], dacc);
+      dacc = T::mfma32(matrix_frag(dt, 2 * s + g), qreg[s], dacc);
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
       float v[4];
