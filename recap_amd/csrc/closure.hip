@@ -52,17 +52,33 @@ __global__ __launch_bounds__(256, 1) void closure_kernel(ClosureArgs a) {
 #pragma unroll
   for (int i = 0; i < (SCAT ? NT : 1); ++i) sacc[i] = f32x16{};
 
+  // The next block's K (and V^T) tile and mean are loaded into registers while this block
+  // is processed, then stored into LDS at the top of the next iteration.
+  constexpr int KCH = G::kTileBytes / 16 / 256;  // 16-byte chunks per thread per tile
+  u32x4 kpre[KCH], vpre[CVK ? KCH : 1];
+  float mpre = 0.0f;
+  auto load_block = [&](int j) {
+    const u32x4* ks = reinterpret_cast<const u32x4*>(a.kp + ((int64_t)bank * a.tb + j) * G::kTileElems);
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) kpre[i] = ks[t + 256 * i];
+    if constexpr (CVK) {
+      const u32x4* vs = reinterpret_cast<const u32x4*>(a.vp + ((int64_t)bank * a.tb + j) * G::kTileElems);
+#pragma unroll
+      for (int i = 0; i < KCH; ++i) vpre[i] = vs[t + 256 * i];
+    }
+    if (t < D) mpre = a.kmean[((int64_t)bank * a.nb + j) * D + t];
+  };
+  if (j0 < j1) load_block(j0);
   for (int j = j0; j < j1; ++j) {
     __syncthreads();
-    {
-      const u32x4* ks = reinterpret_cast<const u32x4*>(a.kp + ((int64_t)bank * a.tb + j) * G::kTileElems);
-      for (int c = t; c < G::kTileBytes / 16; c += 256) reinterpret_cast<u32x4*>(k_lds)[c] = ks[c];
-      if constexpr (CVK) {
-        const u32x4* vs = reinterpret_cast<const u32x4*>(a.vp + ((int64_t)bank * a.tb + j) * G::kTileElems);
-        for (int c = t; c < G::kTileBytes / 16; c += 256) reinterpret_cast<u32x4*>(v_lds)[c] = vs[c];
-      }
-      if (t < D) kmean_s[t] = a.kmean[((int64_t)bank * a.nb + j) * D + t];
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) reinterpret_cast<u32x4*>(k_lds)[t + 256 * i] = kpre[i];
+    if constexpr (CVK) {
+#pragma unroll
+      for (int i = 0; i < KCH; ++i) reinterpret_cast<u32x4*>(v_lds)[t + 256 * i] = vpre[i];
     }
+    if (t < D) kmean_s[t] = mpre;
+    if (j + 1 < j1) load_block(j + 1);
     const int count = min(kBlock, a.n_video - j * kBlock);
     __syncthreads();
 
