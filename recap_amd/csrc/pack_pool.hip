@@ -26,21 +26,42 @@ __global__ __launch_bounds__(256) void pack_pool_kernel(PackPoolArgs a) {
   const bool video_block = tile < a.nb;
   const int count = min(kBlock, a.n_video - tile * kBlock);
 
-  for (int which = 0; which < (PACK ? 2 : 1); ++which) {
-    const uint16_t* src = which == 0 ? a.x0 : a.x1;
-    const int64_t sB = which == 0 ? a.sB0 : a.sB1, sH = which == 0 ? a.sH0 : a.sH1,
-                  sN = which == 0 ? a.sN0 : a.sN1;
-    const uint16_t* base = src + b * sB + h * sH;
+  // Every row load of the block is issued before the first store: the stores go to other
+  // buffers, but the compiler cannot prove it and would otherwise wait for each load in turn.
+  constexpr int NX = PACK ? 2 : 1;
+  u32x4 vals[NX][PASSES];
+  {
+    // Branch-free: rows past the sequence end load row n_tokens - 1 and are zeroed after.
+    int64_t nat[PASSES];
+    bool live[PASSES];
+#pragma unroll
+    for (int i = 0; i < PASSES; ++i) {
+      const int r = tile * kBlock + rl + RP * i;
+      live[i] = r < a.n_tokens;
+      nat[i] = a.rowmap[min(r, a.n_tokens - 1)];
+    }
+#pragma unroll
+    for (int which = 0; which < NX; ++which) {
+      const uint16_t* src = which == 0 ? a.x0 : a.x1;
+      const int64_t sB = which == 0 ? a.sB0 : a.sB1, sH = which == 0 ? a.sH0 : a.sH1,
+                    sN = which == 0 ? a.sN0 : a.sN1;
+      const uint16_t* base = src + b * sB + h * sH;
+#pragma unroll
+      for (int i = 0; i < PASSES; ++i) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(base + nat[i] * sN + cg * 8);
+        vals[which][i] = live[i] ? v : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+  }
+
+#pragma unroll
+  for (int which = 0; which < NX; ++which) {
     float acc[8];
 #pragma unroll
     for (int i = 0; i < PASSES; ++i) {
       const int row = rl + RP * i;
       const int r = tile * kBlock + row;
-      u32x4 val = {0u, 0u, 0u, 0u};
-      if (r < a.n_tokens) {
-        const int64_t nat = a.rowmap[r];
-        val = *reinterpret_cast<const u32x4*>(base + nat * sN + cg * 8);
-      }
+      const u32x4 val = vals[which][i];
       if constexpr (PACK) {
         if (which == 0) {
           char* dst = reinterpret_cast<char*>(a.kp + ((int64_t)bank * a.tb + tile) * G::kTileElems);
