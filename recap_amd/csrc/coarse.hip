@@ -118,7 +118,8 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
   const float half = (float)(0.5 * (double)a.scale * (double)a.scale);
   const float thsq = (float)((double)a.theta * (double)a.theta);
   const float ln_full = logf((float)kBlock);
-  const float ln_last = logf((float)(a.n_video - kBlock * (a.nb - 1)));
+  const float ln_short = logf((float)(a.n_video - kBlock * (a.nb - 1))) - ln_full;  // 0: full
+  const int last_tile = (a.nb - 1) / kCoarseSlots;
 
   // Table tiles (images written by the tables kernel) are copied verbatim into LDS, one
   // tile ahead, by buffer loads over this bank's images; tiles with no omitted block are
@@ -175,7 +176,9 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
         wacc = T::mfma32(lds_load16(w_lds, G::k_off(l32, 4 * ot + 2 * hh + g)), qsq_pk[ot][hh], wacc);
 
     // Lane (g, l32) holds slots mfma_row(rr, g): bits 8 (rr / 4) + 4 g + rr % 4 of the word.
-    // Kept blocks get -inf (branch-free selects).
+    // Kept blocks get -inf (branch-free selects).  The log-count ln 128 common to every full
+    // block is left out of the scores and added to the LSE at the end (softmax, gated share
+    // and output do not depend on it); a short last block gets ln(n / 128) in its own tile.
     const unsigned lb = omit[k] >> (4 * g);
     float sc[16];
     bool gate[16];
@@ -183,16 +186,20 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
 #pragma unroll
     for (int rr = 0; rr < 16; ++rr) {
       const bool om = (lb >> (8 * (rr >> 2) + (rr & 3))) & 1u;
-      const int j = kCoarseSlots * k + mfma_row(rr, g);
       const float quad = wacc[rr];
-      const bool gt = om && quad * ssq <= thsq;
-      float v = sacc[rr] * s32;
-      v = v + (j == a.nb - 1 ? ln_last : ln_full);
-      v = v + (gt ? quad * half : 0.0f);
+      // A kept block's score is -inf, so p = 0 there whatever its gate says.
+      const bool gt = quad * ssq <= thsq;
+      const float v = fmaf(sacc[rr], s32, gt ? quad * half : 0.0f);
       sc[rr] = om ? v : -INFINITY;
       gate[rr] = gt;
-      mx = __builtin_elementwise_maximum(mx, sc[rr]);
     }
+    if (k == last_tile && ln_short != 0.0f) {
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr)
+        if (kCoarseSlots * k + mfma_row(rr, g) == a.nb - 1) sc[rr] += ln_short;
+    }
+#pragma unroll
+    for (int rr = 0; rr < 16; ++rr) mx = __builtin_elementwise_maximum(mx, sc[rr]);
     // Lazy running max: moves only when it grows by more than kTailSlack (p stays < 2^8).
     mx = pair_max(mx);
     const bool grow = mx > m + kTailSlack;
@@ -205,14 +212,15 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
       for (int dt = 0; dt < NDT; ++dt) oacc[dt] *= alpha;
       m = mnew;
     }
+    const float m_log2 = m * kLog2e;
     u32x4 pk[2];
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
       unsigned w[4];
 #pragma unroll
       for (int e = 0; e < 8; e += 2) {
-        const float p0 = __builtin_amdgcn_exp2f((sc[8 * hh + e] - m) * kLog2e);
-        const float p1 = __builtin_amdgcn_exp2f((sc[8 * hh + e + 1] - m) * kLog2e);
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[8 * hh + e], kLog2e, -m_log2));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[8 * hh + e + 1], kLog2e, -m_log2));
         lsum += p0;
         lsum += p1;
         gsum += gate[8 * hh + e] ? p0 : 0.0f;
@@ -270,7 +278,7 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
           u32x2{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3])};
     }
   }
-  const float lse = has_tail ? m + logf(l) : -INFINITY;
+  const float lse = has_tail ? (m + logf(l)) + ln_full : -INFINITY;
   if (g == 0) a.gl[ri] = lse;
   if (a.glref != nullptr) {
     const float diff = half_wave_sum(lse - a.glref[ri]);
