@@ -166,20 +166,39 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
     const char* kb_lds = cur;
     const char* w_lds = kb_lds + kTabBytes;
     const char* vt_lds = kb_lds + 2 * kTabBytes;
+    const unsigned lb = omit[k] >> (4 * g);
+    // The two independent chains s = q.kbar and quad = qsq.w (NS MFMAs each, chunk 2 s + g
+    // of both tiles) interleaved, each slice reading its fragments two slices ahead, so no
+    // MFMA waits on an LDS read issued just before it.
     f32x16 sacc = f32x16{}, wacc = f32x16{};
+    u32x4 kf[3], wf[3];
 #pragma unroll
-    for (int s = 0; s < NS; ++s) sacc = T::mfma32(lds_load16(kb_lds, G::k_off(l32, 2 * s + g)), qreg[s], sacc);
+    for (int s = 0; s < 2; ++s) {
+      kf[s] = lds_load16(kb_lds, G::k_off(l32, 2 * s + g));
+      wf[s] = lds_load16(w_lds, G::k_off(l32, 2 * s + g));
+    }
 #pragma unroll
-    for (int ot = 0; ot < NDT; ++ot)
+    for (int s = 0; s < NS; ++s) {
+      if (s + 2 < NS) {
+        kf[(s + 2) % 3] = lds_load16(kb_lds, G::k_off(l32, 2 * (s + 2) + g));
+        wf[(s + 2) % 3] = lds_load16(w_lds, G::k_off(l32, 2 * (s + 2) + g));
+      }
+      sacc = T::mfma32(kf[s % 3], qreg[s], sacc);
+      wacc = T::mfma32(wf[s % 3], qsq_pk[s >> 1][s & 1], wacc);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // V-bar fragments of the PV product, read now so they are in registers after the softmax.
+    u32x4 vf[NDT][2];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh)
-        wacc = T::mfma32(lds_load16(w_lds, G::k_off(l32, 4 * ot + 2 * hh + g)), qsq_pk[ot][hh], wacc);
+        vf[dt][hh] = lds_load16(vt_lds, coarse_vt_off(32 * dt + l32, 8 * (2 * hh + g)));
 
     // Lane (g, l32) holds slots mfma_row(rr, g): bits 8 (rr / 4) + 4 g + rr % 4 of the word.
     // Kept blocks get -inf (branch-free selects).  The log-count ln 128 common to every full
     // block is left out of the scores and added to the LSE at the end (softmax, gated share
     // and output do not depend on it); a short last block gets ln(n / 128) in its own tile.
-    const unsigned lb = omit[k] >> (4 * g);
     float sc[16];
     bool gate[16];
     float mx = -INFINITY;
@@ -230,12 +249,9 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
       pk[hh] = u32x4{w[0], w[1], w[2], w[3]};
     }
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      const int d = 32 * dt + l32;
+    for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
-        oacc[dt] = T::mfma32(lds_load16(vt_lds, coarse_vt_off(d, 8 * (2 * hh + g))), pk[hh], oacc[dt]);
-    }
+      for (int hh = 0; hh < 2; ++hh) oacc[dt] = T::mfma32(vf[dt][hh], pk[hh], oacc[dt]);
     return kn;
   };
   int k = next_tile(-1);
