@@ -166,7 +166,7 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
     const char* kb_lds = cur;
     const char* w_lds = kb_lds + kTabBytes;
     const char* vt_lds = kb_lds + 2 * kTabBytes;
-    const unsigned lb = omit[k] >> (4 * g);
+    const unsigned ow = __builtin_amdgcn_readfirstlane(omit[k]);
     // The two independent chains s = q.kbar and quad = qsq.w (NS MFMAs each, chunk 2 s + g
     // of both tiles) interleaved, each slice reading its fragments two slices ahead, so no
     // MFMA waits on an LDS read issued just before it.
@@ -195,8 +195,9 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
       for (int hh = 0; hh < 2; ++hh)
         vf[dt][hh] = lds_load16(vt_lds, coarse_vt_off(32 * dt + l32, 8 * (2 * hh + g)));
 
-    // Lane (g, l32) holds slots mfma_row(rr, g): bits 8 (rr / 4) + 4 g + rr % 4 of the word.
-    // Kept blocks get -inf (branch-free selects).  The log-count ln 128 common to every full
+    // Lane (g, l32) holds slots mfma_row(rr, g): bits 8 (rr / 4) + 4 g + rr % 4 of the word,
+    // the same for the 32 lanes of a half-wave, so each slot's omitted flag is a wave mask
+    // built on the scalar unit.  Kept blocks get -inf (branch-free selects).  The log-count ln 128 common to every full
     // block is left out of the scores and added to the LSE at the end (softmax, gated share
     // and output do not depend on it); a short last block gets ln(n / 128) in its own tile.
     float sc[16];
@@ -204,7 +205,10 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
     float mx = -INFINITY;
 #pragma unroll
     for (int rr = 0; rr < 16; ++rr) {
-      const bool om = (lb >> (8 * (rr >> 2) + (rr & 3))) & 1u;
+      const int sh = 8 * (rr >> 2) + (rr & 3);
+      const bool om = __builtin_amdgcn_inverse_ballot_w64(
+          (((ow >> sh) & 1u) ? 0x00000000ffffffffull : 0ull) |
+          (((ow >> (sh + 4)) & 1u) ? 0xffffffff00000000ull : 0ull));
       const float quad = wacc[rr];
       // A kept block's score is -inf, so p = 0 there whatever its gate says.
       const bool gt = quad * ssq <= thsq;
