@@ -181,6 +181,21 @@ int recap_block_sparse_attn(const void* q, int dtype, int64_t batch, int64_t hea
                             const uint8_t* kernel_mask, int64_t n_tokens, float scale,
                             float* head_out, float* head_lse, void* stream);
 
+/* A refresh's two attention results in one pass over the keys: the dense output and LSE
+ * as recap_dense_attn, and the head branch of `kernel_mask` as recap_block_sparse_attn
+ * (head_out [banks, n_tokens, dim] fp32 and head_lse [banks, n_tokens], reordered rows).
+ * Each query block walks its kept key blocks first and stores the head branch from the
+ * running softmax state when they are done, then walks the rest.
+ * Replaces the two attention calls of a refresh: aten._scaled_dot_product_flash_attention,
+ * recap/operator.py:254-256, and block_sparse_exact, recap/operator.py:345-346 with
+ * recap/kernels/block_sparse.py:78-139. */
+int recap_dense_head_attn(const void* q, int dtype, int64_t batch, int64_t heads, int64_t dim,
+                          int64_t stride_b, int64_t stride_h, int64_t stride_n,
+                          const void* k_tiles, const void* vt_tiles, const int32_t* rowmap,
+                          const uint8_t* kernel_mask, int64_t n_tokens, float scale, void* out,
+                          int64_t out_stride_b, int64_t out_stride_h, int64_t out_stride_n,
+                          float* lse, float* head_out, float* head_lse, void* stream);
+
 /* Dense attention with LSE, native order: out [batch, heads, n_tokens, dim] with the
  * given strides, lse [banks, n_tokens].
  * Replaces aten._scaled_dot_product_flash_attention at recap/operator.py:254-256. */

@@ -49,6 +49,8 @@ SIGNATURES: dict[str, tuple] = {
                                      _F, _P, _P, _P]),
     "recap_dense_attn": (_I, [_P, _I, _I64, _I64, _I64, *_STRIDES, _P, _P, _P, _I64, _F, _P,
                               *_STRIDES, _P, _P]),
+    "recap_dense_head_attn": (_I, [_P, _I, _I64, _I64, _I64, *_STRIDES, _P, _P, _P, _P, _I64, _F,
+                                   _P, *_STRIDES, _P, _P, _P, _P]),
     "recap_sparse_merge_attn": (_I, [_P, _I, _I64, _I64, _I64, *_STRIDES, _P, _P, _P, _P, _I64,
                                      _I64, _F, _P, _P, _P, _P, _P, _P, _F, _P, *_STRIDES, _P]),
     "recap_capture_partials": (_I64, [_I64, _I64, _I64]),

@@ -432,6 +432,27 @@ int recap_dense_attn(const void* q, int dtype, int64_t batch, int64_t heads, int
   return hip_status(run_attention(a, dtype, (int)dim, kModeDense, as_stream(stream)), "attention launch");
 }
 
+int recap_dense_head_attn(const void* q, int dtype, int64_t batch, int64_t heads, int64_t dim,
+                          int64_t stride_b, int64_t stride_h, int64_t stride_n,
+                          const void* k_tiles, const void* vt_tiles, const int32_t* rowmap,
+                          const uint8_t* kernel_mask, int64_t n_tokens, float scale, void* out,
+                          int64_t out_stride_b, int64_t out_stride_h, int64_t out_stride_n,
+                          float* lse, float* head_out, float* head_lse, void* stream) {
+  AttnArgs a{};
+  CHECK(attn_common(q, dtype, batch, heads, dim, stride_b, stride_h, stride_n, k_tiles, vt_tiles,
+                    rowmap, n_tokens, n_tokens, a));
+  CHECK(check_qkv("out", out, batch, heads, out_stride_b, out_stride_h, out_stride_n));
+  REQUIRE(kernel_mask != nullptr, "kernel_mask is NULL");
+  REQUIRE(lse != nullptr && head_out != nullptr && head_lse != nullptr, "lse/head_out/head_lse NULL");
+  a.kmask = kernel_mask;
+  a.ds = a.tb;  // every query block walks all tb blocks: no long items to start first
+  a.scale_log2 = scale * kLog2e;
+  a.out = static_cast<uint16_t*>(out); a.osB = out_stride_b; a.osH = out_stride_h; a.osN = out_stride_n;
+  a.lse_native = lse;
+  a.head_out = head_out; a.head_lse = head_lse;
+  return hip_status(run_attention(a, dtype, (int)dim, kModeDenseHead, as_stream(stream)), "attention launch");
+}
+
 int recap_sparse_merge_attn(const void* q, int dtype, int64_t batch, int64_t heads,
                             int64_t dim, int64_t stride_b, int64_t stride_h, int64_t stride_n,
                             const void* k_tiles, const void* vt_tiles, const int32_t* rowmap,

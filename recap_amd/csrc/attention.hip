@@ -17,6 +17,9 @@
 // Epilogues:
 //   head   (oh fp32, lh) in reordered order -- the head branch a refresh capture needs;
 //   dense  output + LSE in native order -- a refresh's dense call;
+//   dense-head  both of a refresh in one pass: the kept blocks are walked first, the head
+//          branch is stored when they are done (bit-identical to the head mode's result),
+//          then the remaining blocks complete the dense output;
 //   merge  head (+) [coarse tail + drift-weighted refinement] in LSE space for rows < R,
 //          the head alone above (recap/kernels/detail_cache.py:220-301), written in
 //          native order: the whole corrected sparse output in one pass.
@@ -182,6 +185,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
 
   int nkeep = a.tb;
   if constexpr (MODE != kModeDense) {
+    // Kept blocks in ascending order; in dense-head mode the other blocks follow them.
     const uint8_t* mrow = a.kmask + ((int64_t)bank * a.tb + qt) * a.tb;
     const int per = (a.tb + kThreads - 1) / kThreads;
     const int j0 = min(t * per, a.tb), j1 = min(j0 + per, a.tb);
@@ -196,12 +200,21 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
       __syncthreads();
     }
     int pos = scan[t] - cnt;
-    for (int j = j0; j < j1; ++j)
-      if (mrow[j]) list[pos++] = j;
-    nkeep = scan[kThreads - 1];
+    nkeep = __builtin_amdgcn_readfirstlane(scan[kThreads - 1]);
+    int npos = nkeep + (j0 - pos);  // blocks not kept before this thread's range
+    // Dense-head mode puts a kept ragged last block first, so its masked steps open the walk.
+    const bool lead = MODE == kModeDenseHead && (a.n_tokens % kBlock) != 0 && mrow[a.tb - 1] != 0;
+    for (int j = j0; j < j1; ++j) {
+      if (mrow[j]) {
+        list[lead ? (j == a.tb - 1 ? 0 : pos + 1) : pos] = j;
+        ++pos;
+      } else if (MODE == kModeDenseHead) {
+        list[npos++] = j;
+      }
+    }
     __syncthreads();
   }
-  const int nsub = 2 * nkeep;  // 64-key sub-tiles
+  const int nsub = MODE == kModeDenseHead ? 2 * a.tb : 2 * nkeep;  // 64-key sub-tiles
 
   // Sub-tile `it` = half (it & 1) of kept tile (it >> 1): its K rows and its V^T half are
   // each HALF contiguous bytes of the packed images, copied verbatim into LDS slot it & 1
@@ -318,7 +331,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
   // The matrix core then works while the VALU does, instead of one after the other.
   // `it` is even at every call with parity tag 0 and odd with tag 1.
   auto step = [&](int it, f32x16 (&cur)[kGroups][2], f32x16 (&nxt)[kGroups][2], auto mask_tag,
-                  auto next_tag, auto parity_tag) {
+                  auto next_tag, auto parity_tag) __attribute__((always_inline)) {
     constexpr bool kNext = decltype(next_tag)::value;
     constexpr bool kMask = decltype(mask_tag)::value;
     constexpr bool kOdd = decltype(parity_tag)::value;
@@ -401,43 +414,73 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
     tile_barrier();
   };
 
-  // The last kept tile holds the ragged keys when it is the sequence's last block.
-  const bool ragged_last = ragged && nkeep > 0 &&
-                           (MODE == kModeDense ? true : list[nkeep - 1] == a.tb - 1);
-  const int plain = ragged_last ? nsub - 2 : nsub;  // sub-tiles below this need no mask
+  // True when sub-tile `it` of the list lies in the ragged last block.
+  auto ragged_at = [&](int it) {
+    const int j = MODE == kModeDense ? (it >> 1) : __builtin_amdgcn_readfirstlane(list[it >> 1]);
+    return ragged && j == a.tb - 1;
+  };
   f32x16 sa[kGroups][2], sb[kGroups][2];
   if (nsub > 0) {
     qk(k_lds0, sa);
-    if (plain == 0) mask_tail(sa, 0);
+    if (ragged_at(0)) mask_tail(sa, 0);
     row_max(sa);
     tile_barrier();  // step 0 overwrites K slot 0 (read just now)
   }
   using F = std::false_type;
   using Tr = std::true_type;
-  // nsub is even, so steps go in pairs (even step: S in sa -> sb, odd step: sb -> sa) and
-  // each array keeps one role.  The last two pairs are peeled: they compute S of the last
-  // kept tile, which is masked when it is the ragged final block, and the final step has
-  // no next sub-tile.
+  // Dense-head mode: the head branch of the kept blocks (the list's first 2 * nkeep
+  // sub-tiles), stored from the running state once their last PV is done.
+  const int kept_end = 2 * nkeep;
+  auto snapshot = [&](int done) __attribute__((always_inline)) {
+    if constexpr (MODE == kModeDenseHead) {
+      if (done == kept_end) {
+#pragma unroll
+        for (int q = 0; q < kGroups; ++q) {
+          const float lt = pair_sum(lsum[q]);
+          if (valid[q])
+            store_rows<T, D, kModeHead>(a, bank, b, h, row[q], nat[q], g, oacc[q], m[q], lt);
+        }
+      }
+    }
+  };
+  // Steps go in pairs (even step: S in sa -> sb, odd step: sb -> sa) so each array keeps one
+  // role.  Step it computes S of sub-tile it + 1, masked when that sub-tile lies in the ragged
+  // last block: only the last two pairs (the ragged block last) and, in dense-head mode, the
+  // first pair (a kept ragged block goes first) can meet it, so those are peeled and the main
+  // loop runs unmasked.  The final step has no next sub-tile.
+  snapshot(0);
   int it = 0;
+  if constexpr (MODE == kModeDenseHead) {
+    if (nsub >= 4) {
+      if (ragged_at(1)) step(0, sa, sb, Tr{}, Tr{}, F{}); else step(0, sa, sb, F{}, Tr{}, F{});
+      if (ragged_at(2)) step(1, sb, sa, Tr{}, Tr{}, Tr{}); else step(1, sb, sa, F{}, Tr{}, Tr{});
+      snapshot(2);
+      it = 2;
+    }
+  }
   for (; it + 4 < nsub; it += 2) {
     step(it, sa, sb, F{}, Tr{}, F{});
     step(it + 1, sb, sa, F{}, Tr{}, Tr{});
+    snapshot(it + 2);
   }
-  if (nsub >= 4) {
+  if (nsub - it >= 4) {
     step(it, sa, sb, F{}, Tr{}, F{});
-    if (ragged_last) step(it + 1, sb, sa, Tr{}, Tr{}, Tr{});
+    if (ragged_at(it + 2)) step(it + 1, sb, sa, Tr{}, Tr{}, Tr{});
     else step(it + 1, sb, sa, F{}, Tr{}, Tr{});
+    snapshot(it + 2);
     it += 2;
   }
   if (nsub >= 2) {
-    if (ragged_last) step(it, sa, sb, Tr{}, Tr{}, F{}); else step(it, sa, sb, F{}, Tr{}, F{});
+    if (ragged_at(it + 1)) step(it, sa, sb, Tr{}, Tr{}, F{}); else step(it, sa, sb, F{}, Tr{}, F{});
     step(it + 1, sb, sa, F{}, F{}, Tr{});
+    snapshot(nsub);
   }
 
+  constexpr int kStore = MODE == kModeDenseHead ? kModeDense : MODE;
 #pragma unroll
   for (int q = 0; q < kGroups; ++q) {
     const float lt = pair_sum(lsum[q]);  // lanes l and l ^ 32 share one row: both valid or not
-    if (valid[q]) store_rows<T, D, MODE>(a, bank, b, h, row[q], nat[q], g, oacc[q], m[q], lt);
+    if (valid[q]) store_rows<T, D, kStore>(a, bank, b, h, row[q], nat[q], g, oacc[q], m[q], lt);
   }
 }
 
@@ -447,6 +490,7 @@ static hipError_t launch_attention(const AttnArgs& a, int mode, hipStream_t s) {
   switch (mode) {
     case kModeHead: hipLaunchKernelGGL((attention_kernel<T, D, kModeHead>), grid, block, 0, s, a); break;
     case kModeDense: hipLaunchKernelGGL((attention_kernel<T, D, kModeDense>), grid, block, 0, s, a); break;
+    case kModeDenseHead: hipLaunchKernelGGL((attention_kernel<T, D, kModeDenseHead>), grid, block, 0, s, a); break;
     default: hipLaunchKernelGGL((attention_kernel<T, D, kModeMerge>), grid, block, 0, s, a); break;
   }
   return hipGetLastError();

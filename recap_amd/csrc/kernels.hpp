@@ -79,16 +79,16 @@ struct CoarseArgs {
 hipError_t run_coarse(const CoarseArgs& a, int dtype, int dim, hipStream_t s);
 
 // Block-sparse attention (attention.hip).
-enum AttnMode { kModeHead = 0, kModeDense = 1, kModeMerge = 2 };
+enum AttnMode { kModeHead = 0, kModeDense = 1, kModeMerge = 2, kModeDenseHead = 3 };
 struct AttnArgs {
   const uint16_t* q; int64_t qsB, qsH, qsN;
   const uint16_t* kp; const uint16_t* vp;
   const int32_t* rowmap; const uint8_t* kmask;   // kmask null in dense mode
   int heads, banks, n_tokens, tb, ds;
   float scale_log2;
-  float* head_out; float* head_lse;              // head mode, reordered [bank][N](D), fp32
-  uint16_t* out; int64_t osB, osH, osN;          // dense / merge, native order
-  float* lse_native;                             // dense mode [bank][N]
+  float* head_out; float* head_lse;              // head / dense-head, reordered [bank][N](D), fp32
+  uint16_t* out; int64_t osB, osH, osN;          // dense / dense-head / merge, native order
+  float* lse_native;                             // dense / dense-head [bank][N]
   int rows; const uint16_t* go; const float* gl; const uint16_t* det; const float* dl;
   const float* glref; const float* center; float alpha_override; int use_override;
 };

@@ -342,6 +342,25 @@ def dense_attn(q: torch.Tensor, kv: PackedKV, rowmap: torch.Tensor, scale: float
     return out, lse
 
 
+def dense_head_attn(q: torch.Tensor, kv: PackedKV, rowmap: torch.Tensor,
+                    kernel_mask: torch.Tensor, scale: float, out: torch.Tensor | None = None):
+    """A refresh's dense attention and head branch in one pass:
+    (out [B, H, N, d] native, lse [B, H, N], head_out [banks, N, d] fp32 reordered,
+    head_lse [banks, N])."""
+    b, h, n, d = q.shape
+    kernel_mask = kernel_mask.contiguous()
+    if out is None:
+        out = torch.empty(b, h, n, d, dtype=q.dtype, device=q.device)
+    lse = torch.empty(b, h, n, dtype=torch.float32, device=q.device)
+    head_out = torch.empty(b * h, n, d, dtype=torch.float32, device=q.device)
+    head_lse = torch.empty(b * h, n, dtype=torch.float32, device=q.device)
+    call("recap_dense_head_attn", *_qkv_args(q), kv.k_tiles.data_ptr(), kv.vt_tiles.data_ptr(),
+         rowmap.data_ptr(), kernel_mask.data_ptr(), n, float(scale), out.data_ptr(),
+         out.stride(0), out.stride(1), out.stride(2), lse.data_ptr(), head_out.data_ptr(),
+         head_lse.data_ptr(), _stream())
+    return out, lse, head_out, head_lse
+
+
 def sparse_merge_attn(q: torch.Tensor, kv: PackedKV, rowmap: torch.Tensor,
                       kernel_mask: torch.Tensor, geo: Geometry, scale: float, go, gl, det, dl,
                       glref, center, alpha_override: float | None = None,

@@ -264,8 +264,14 @@ class Operator:
         if self.kind == SPARSE:
             return self._sparse(layer, bank, q, k, v, geo, rowmap)
         kv = K.kv_pack(k, v, rowmap, geo)
-        out, lse = K.dense_attn(q, kv, rowmap, K.scale_for(q.shape[-1]))
-        self._refresh(layer, bank, q, kv, geo, rowmap, out, lse)
+        # The head branch comes out of the dense pass: its mask is the stored one, or on a
+        # bank's first refresh the selection made now.
+        selection = None if bank.valid else self._select(layer, q, kv, geo, rowmap)
+        kmask = bank.head_kernel_mask if selection is None else selection[1]
+        out, lse, head_out, head_lse = K.dense_head_attn(q, kv, rowmap, kmask,
+                                                         K.scale_for(q.shape[-1]))
+        self._refresh(layer, bank, q, kv, geo, rowmap, out, lse, head=(head_out, head_lse),
+                      selection=selection)
         return out
 
     @torch.no_grad()
@@ -277,10 +283,16 @@ class Operator:
         rowmap = self.layout.rowmap(q.device)
         bank = self.banks[self.stream][layer_index]
         out = torch.empty(b, h, n, d, dtype=q.dtype, device=q.device)
-        lse = None
+        lse = head_all = selection_all = None
         if self.kind == REFRESH:
             kv_all = K.kv_pack(k, v, rowmap, geo)
-            _, lse = K.dense_attn(q, kv_all, rowmap, K.scale_for(d), out=out)
+            if not bank.valid:
+                selection_all = self._select(self.layers[self.stream][layer_index], q, kv_all,
+                                             geo, rowmap)
+            kmask = bank.head_kernel_mask if selection_all is None else selection_all[1]
+            _, lse, head_out, head_lse = K.dense_head_attn(q, kv_all, rowmap, kmask,
+                                                           K.scale_for(d), out=out)
+            head_all = (head_out, head_lse)
             del kv_all
         forced = None
         if self.kind == REFRESH and bank.valid and bank.partition is not None:
@@ -313,8 +325,12 @@ class Operator:
                     self._sparse(state, view, qs, ks, vs, geo, rowmap, out=out[bi:bi + 1, h0:h1])
                 else:
                     kv = K.kv_pack(ks, vs, rowmap, geo)
+                    lo, hi = bi * h + h0, bi * h + h1
+                    sel = None if selection_all is None else (
+                        selection_all[0][bi:bi + 1, h0:h1], selection_all[1][lo:hi])
                     self._refresh(state, view, qs, kv, geo, rowmap, out[bi:bi + 1, h0:h1],
-                                  lse[bi:bi + 1, h0:h1])
+                                  lse[bi:bi + 1, h0:h1],
+                                  head=(head_all[0][lo:hi], head_all[1][lo:hi]), selection=sel)
                 group += 1
         self._forced_partition = None
         self._forced_rerank = None
@@ -334,15 +350,24 @@ class Operator:
         return part.reshape(b, h, geo.nb, geo.nb), kmask
 
     @torch.no_grad()
-    def _refresh(self, layer, bank, q, kv, geo, rowmap, full_output, full_lse) -> None:
-        """Store the refinement and measure the previous one (recap/operator.py:330-473)."""
+    def _refresh(self, layer, bank, q, kv, geo, rowmap, full_output, full_lse, head=None,
+                 selection=None) -> None:
+        """Store the refinement and measure the previous one (recap/operator.py:330-473).
+
+        ``head`` is the head branch of the bank's current (or, on a first refresh, newly
+        selected ``selection``) mask when the dense pass already produced it."""
         b, h, n, d = q.shape
         banks = b * h
         scale = K.scale_for(d)
         revalidating = bank.valid
         if not revalidating:
-            bank.partition, bank.head_kernel_mask = self._select(layer, q, kv, geo, rowmap)
-        head_out, head_lse = K.block_sparse_attn(q, kv, rowmap, bank.head_kernel_mask, geo, scale)
+            bank.partition, bank.head_kernel_mask = (
+                selection if selection is not None else self._select(layer, q, kv, geo, rowmap))
+        if head is not None:
+            head_out, head_lse = head
+        else:
+            head_out, head_lse = K.block_sparse_attn(q, kv, rowmap, bank.head_kernel_mask, geo,
+                                                     scale)
         context = layer.coarse_tail_context(kv, geo)
         flat_part = bank.partition.reshape(banks, geo.nb, geo.nb)
         old_lse = bank.coarse_lse if revalidating else None

@@ -104,6 +104,43 @@ def test_head_and_dense_attention(cuda, name):
     assert m < 2e-3, m
 
 
+@pytest.mark.parametrize("name", list(SMALL))
+def test_dense_head_attention_one_pass(cuda, name):
+    """The refresh's fused pass: its dense part against the oracle's dense attention and the
+    dense kernel, its head part (stored mid-walk) against the oracle's block-sparse attention
+    and the head kernel, for masks whose kept ragged block goes first."""
+    wl, (q, k, v), (qg, kg, vg), rowmap, fwd, geo = _setup(name, None, cuda)
+    scale = scale_for(wl.dim)
+    kv = K.kv_pack(kg, vg, rowmap, geo)
+    ql, kl, vl = (banks_view(x, fwd) for x in (q, k, v))
+    part_ref = O.head_partition(ql, kl, scale, wl.density, wl.video_tokens)
+    kmask_ref = O.kernel_block_mask(part_ref, wl.tokens, wl.video_tokens)
+    dense, dlse, hout, hlse = K.dense_head_attn(qg, kv, rowmap, kmask_ref.to(cuda), scale)
+    ref, ref_lse = O.block_sparse_attention(ql, kl, vl, kmask_ref, scale)
+    assert_close_bf16(hout.cpu().float(), ref, f"fused head {name}")
+    m, _ = metrics(hlse.cpu(), ref_lse)
+    assert m < 2e-3, m
+    # Same kept blocks, but a kept ragged block goes first here and the running max may
+    # also move with the first block after the kept ones: P, rounded to bf16 for the PV
+    # product, is rounded under another max, so the two agree to the bf16 precision of P;
+    # the LSE to fp32 rounding.
+    alone, alone_lse = K.block_sparse_attn(qg, kv, rowmap, kmask_ref.to(cuda), geo, scale)
+    m, _ = metrics(hout.cpu(), alone.cpu())
+    print(f"  fused head vs head kernel (fp32): max_abs {m:.2e}", flush=True)
+    assert m < 2e-2
+    assert float((hlse - alone_lse).abs().max()) < 1e-4
+    dref, dref_lse = O.dense_attention(ql, kl, vl, scale)
+    _, inv = O.gather_indices(hilbert_permutation(wl.grid), wl.text_tokens, wl.text_first)
+    b, h = q.shape[:2]
+    assert_close_bf16(dense.cpu().float(), O.restore(dref.reshape(b, h, -1, wl.dim), inv),
+                      f"fused dense {name}")
+    m, _ = metrics(dlse.cpu(), dref_lse.reshape(b, h, -1).index_select(-1, inv))
+    assert m < 2e-3, m
+    dense2, dlse2 = K.dense_attn(qg, kv, rowmap, scale)
+    assert float((dense.float() - dense2.float()).abs().max()) <= 2e-2
+    assert float((dlse - dlse2).abs().max()) < 1e-4
+
+
 def test_dense_attention_matches_torch_sdpa(cuda):
     wl = SMALL["text-last-d128"]
     q, k, v = (x.to(cuda) for x in make_qkv(wl, seed=1))
