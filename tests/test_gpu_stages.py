@@ -141,6 +141,40 @@ def test_dense_head_attention_one_pass(cuda, name):
     assert float((dlse - dlse2).abs().max()) < 1e-4
 
 
+@pytest.mark.parametrize("n,d,keep_last", [(100, 64, True), (200, 128, True), (200, 128, False),
+                                          (300, 64, False), (384, 128, True), (700, 128, False)])
+def test_attention_modes_short_and_ragged(cuda, n, d, keep_last):
+    """Head, dense and dense-head modes on one to six blocks, with the ragged last block kept
+    (walked first in dense-head mode) or not kept (walked last), against the oracle."""
+    print(f"case n={n} d={d} keep_last={keep_last}", flush=True)
+    g = torch.Generator().manual_seed(n + d)
+    banks, tb = 2, -(-n // 128)
+    q, k, v = (torch.randn(1, banks, n, d, generator=g).to(torch.bfloat16) for _ in range(3))
+    kmask = torch.rand(banks, tb, tb, generator=g) > 0.5
+    kmask[:, torch.arange(tb), torch.arange(tb)] = True
+    kmask[:, :, -1] = keep_last
+    if not keep_last:
+        kmask[:, -1, -1] = True   # the last row keeps at least its own block
+    geo = K.Geometry(n, n)
+    rowmap = torch.arange(n, dtype=torch.int32, device=cuda)
+    kv = K.kv_pack(k.to(cuda), v.to(cuda), rowmap, geo)
+    scale = scale_for(d)
+    ql, kl, vl = (x[0].float() for x in (q, k, v))
+    ref, ref_lse = O.block_sparse_attention(ql, kl, vl, kmask, scale)
+    dref, dref_lse = O.dense_attention(ql, kl, vl, scale)
+    head, head_lse = K.block_sparse_attn(q.to(cuda), kv, rowmap, kmask.to(cuda), geo, scale)
+    assert_close_bf16(head.cpu().float(), ref, "head")
+    dense, dlse = K.dense_attn(q.to(cuda), kv, rowmap, scale)
+    assert_close_bf16(dense.cpu().float()[0], dref, "dense")
+    fd, flse, fh, fhlse = K.dense_head_attn(q.to(cuda), kv, rowmap, kmask.to(cuda), scale)
+    assert_close_bf16(fh.cpu().float(), ref, "dense-head: head")
+    assert_close_bf16(fd.cpu().float()[0], dref, "dense-head: dense")
+    for got, want in ((head_lse, ref_lse), (fhlse, ref_lse), (dlse[0], dref_lse),
+                      (flse[0], dref_lse)):
+        m, _ = metrics(got.cpu(), want)
+        assert m < 2e-3, m
+
+
 def test_dense_attention_matches_torch_sdpa(cuda):
     wl = SMALL["text-last-d128"]
     q, k, v = (x.to(cuda) for x in make_qkv(wl, seed=1))
