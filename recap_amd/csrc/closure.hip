@@ -20,7 +20,7 @@ __global__ __launch_bounds__(256, 1) void closure_kernel(ClosureArgs a) {
   using G = TileGeom<D>;
   constexpr int NS = D / 16, NT = D / 32;
   constexpr bool ROT = (FLAGS & kRot) != 0, CVK = (FLAGS & kCvk) != 0, SCAT = (FLAGS & kScatter) != 0;
-  constexpr bool KC = CVK || SCAT;
+  constexpr bool KC = SCAT;  // centred keys staged in LDS (the scatter's A and B operands)
   __shared__ __attribute__((aligned(16))) char k_lds[G::kTileBytes];
   __shared__ __attribute__((aligned(16))) char v_lds[CVK ? G::kTileBytes : 16];
   __shared__ __attribute__((aligned(16))) char kc_hi[KC ? D * 256 : 16];
@@ -45,6 +45,16 @@ __global__ __launch_bounds__(256, 1) void closure_kernel(ClosureArgs a) {
         ub_lo[s] = *reinterpret_cast<const u32x4*>(lo + 16 * s + 8 * g);
       }
     }
+  }
+  // Identity slices for the centred-key product: B operand hh holds 1 where key-dimension
+  // 16 hh + 8 g + e equals this lane's column l32 (e = 0..7), 0 elsewhere.
+  u32x4 bid[2];
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+    const int e = l32 - 16 * hh - 8 * g;
+    const unsigned one = (T::code == BF16::code ? 0x3f80u : 0x3c00u) << (16 * (e & 1));
+    bid[hh] = u32x4{e >> 1 == 0 ? one : 0u, e >> 1 == 1 ? one : 0u, e >> 1 == 2 ? one : 0u,
+                    e >> 1 == 3 ? one : 0u};
   }
   f32x16 cacc[CVK ? NT : 1], sacc[SCAT ? NT : 1];
 #pragma unroll
@@ -152,16 +162,48 @@ __global__ __launch_bounds__(256, 1) void closure_kernel(ClosureArgs a) {
 
     if constexpr (CVK) {
       if (mat_tile >= 0) {
-        const int mrow = 32 * mat_tile + l32;
+        // C_vk[:, n] for this wave's 32 columns n.  The centred keys come from the matrix
+        // core: the K rows times an identity slice, accumulated onto -kbar[n], land in the
+        // output layout (lane = column n, registers = 16 tokens in swap23 order), which is
+        // the B operand of V^T Kc against the V^T tile's positions -- no transpose in LDS.
+        const float neg_mean = -kmean_s[32 * mat_tile + l32];
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          const u32x4 va = lds_load16(v_lds, G::vt_off(mrow, 2 * s + g));
+        for (int tt = 0; tt < 4; ++tt) {
+          f32x16 kc;
 #pragma unroll
-          for (int nt = 0; nt < NT; ++nt) {
-            const int off = G::vt_off(32 * nt + l32, 2 * s + g);
-            cacc[nt] = T::mfma32(va, lds_load16(kc_hi, off), cacc[nt]);
-            cacc[nt] = T::mfma32(va, lds_load16(kc_lo, off), cacc[nt]);
+          for (int r = 0; r < 16; ++r) kc[r] = neg_mean;
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh)
+            kc = T::mfma32(lds_load16(k_lds, G::k_off(32 * tt + l32, 4 * mat_tile + 2 * hh + g)),
+                           bid[hh], kc);
+          if (count < kBlock) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+              if (32 * tt + mfma_row(r, g) >= count) kc[r] = 0.0f;
           }
+          // hi + lo pair of the centred key, as in the staged path.
+          u32x4 bhi[2], blo[2];
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            unsigned whi[4], wlo[4];
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+              const float x0 = kc[8 * hh + e], x1 = kc[8 * hh + e + 1];
+              const float h0 = T::to_f(T::from_f(x0)), h1 = T::to_f(T::from_f(x1));
+              whi[e >> 1] = pack2<T>(h0, h1);
+              wlo[e >> 1] = pack2<T>(x0 - h0, x1 - h1);
+            }
+            bhi[hh] = u32x4{whi[0], whi[1], whi[2], whi[3]};
+            blo[hh] = u32x4{wlo[0], wlo[1], wlo[2], wlo[3]};
+          }
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int mt = 0; mt < NT; ++mt) {
+              const u32x4 va = lds_load16(v_lds, G::vt_off(32 * mt + l32, 4 * tt + 2 * hh + g));
+              cacc[mt] = T::mfma32(va, bhi[hh], cacc[mt]);
+              cacc[mt] = T::mfma32(va, blo[hh], cacc[mt]);
+            }
         }
       }
     }
@@ -191,9 +233,14 @@ __global__ __launch_bounds__(256, 1) void closure_kernel(ClosureArgs a) {
     for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
       for (int rr = 0; rr < 16; ++rr) {
-        const int64_t off = pbase + (int64_t)(32 * mat_tile + mfma_row(rr, g)) * D + 32 * nt + l32;
-        if constexpr (CVK) a.cvk_part[off] = cacc[nt][rr];
-        if constexpr (SCAT) a.scat_part[off] = sacc[nt][rr];
+        // cacc[nt]: rows m of tile nt, this wave's columns; sacc[nt]: this wave's rows n,
+        // columns of tile nt.
+        if constexpr (CVK)
+          a.cvk_part[pbase + (int64_t)(32 * nt + mfma_row(rr, g)) * D + 32 * mat_tile + l32] =
+              cacc[nt][rr];
+        if constexpr (SCAT)
+          a.scat_part[pbase + (int64_t)(32 * mat_tile + mfma_row(rr, g)) * D + 32 * nt + l32] =
+              sacc[nt][rr];
       }
   }
 }
