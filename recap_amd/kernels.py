@@ -41,6 +41,9 @@ class Geometry:
 
     n_tokens: int
     n_video: int
+    # Video blocks per closure-statistics workgroup, fixed for a whole layer (the partial
+    # sums, and so the rounding, depend on it); None: chosen from the call's banks.
+    closure_group: int | None = None
 
     @property
     def nb(self) -> int:
@@ -200,10 +203,18 @@ def select_blocks(q: torch.Tensor, k_means: torch.Tensor, rowmap: torch.Tensor, 
 CLOSURE_GROUP = 8
 
 
+def closure_group(banks: int, nb: int) -> int:
+    """Video blocks per closure workgroup: up to CLOSURE_GROUP, fewer when the call has too
+    few blocks to give every CU several workgroups (about 1024 in all)."""
+    return max(1, min(CLOSURE_GROUP, (banks * nb) // 1024))
+
+
 def closure_stats(kv: PackedKV, geo: Geometry, flags: int, u_hi_t=None, u_lo_t=None,
-                  group: int = CLOSURE_GROUP):
+                  group: int | None = None):
     """(variance, C_vk, scatter) for the requested statistics; absent ones are None."""
     banks, d = kv.k_means.shape[0], kv.dim
+    if group is None:
+        group = geo.closure_group or closure_group(banks, geo.nb)
     dev = kv.k_means.device
     groups = int(_lib.load().recap_closure_groups(geo.n_video, group))
     var = cvk_part = scat_part = None

@@ -242,7 +242,10 @@ class Operator:
 
     def _geometry(self, query: torch.Tensor) -> K.Geometry:
         self.layout._check(query)
-        return K.Geometry(n_tokens=query.shape[-2], n_video=self.layout.video_tokens)
+        banks = query.shape[0] * query.shape[1]
+        nb = -(-self.layout.video_tokens // K.BLOCK)
+        return K.Geometry(n_tokens=query.shape[-2], n_video=self.layout.video_tokens,
+                          closure_group=K.closure_group(banks, nb))
 
     @torch.no_grad()
     def attend(self, layer_index: int, query: torch.Tensor, key: torch.Tensor,
