@@ -23,8 +23,6 @@ namespace recap {
 
 constexpr int kMaxVideoBlocks = 4096;
 
-constexpr float kTailSlack = 8.0f * kLn2;      // lazy-max slack, natural-log units
-
 template <class T, int D>
 __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
 #pragma clang fp contract(off)
@@ -117,9 +115,23 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
   const float ssq = (float)((double)a.scale * (double)a.scale);
   const float half = (float)(0.5 * (double)a.scale * (double)a.scale);
   const float thsq = (float)((double)a.theta * (double)a.theta);
+  // The gate fl(quad * s^2) <= theta^2 as one compare quad <= thq: fl(x * s^2) is monotone in
+  // x, so the quads that pass form (-inf, thq], with thq within an ulp or two of
+  // theta^2 / s^2 (found by stepping; exact for every scale, not only powers of two).
+  float thq = thsq / ssq;
+  for (int i = 0; i < 4 && thq * ssq > thsq; ++i) thq = nextafterf(thq, -INFINITY);
+  for (int i = 0; i < 4 && nextafterf(thq, INFINITY) * ssq <= thsq; ++i)
+    thq = nextafterf(thq, INFINITY);
+  // Scores in log2 units: c1 on q.kbar, c2 on the gated qsq.w term.
+  const float c1 = s32 * kLog2e, c2 = half * kLog2e;
   const float ln_full = logf((float)kBlock);
-  const float ln_short = logf((float)(a.n_video - kBlock * (a.nb - 1))) - ln_full;  // 0: full
+  const float short2 = (logf((float)(a.n_video - kBlock * (a.nb - 1))) - ln_full) * kLog2e;
   const int last_tile = (a.nb - 1) / kCoarseSlots;
+  // Block nb - 1 sits in slot sl = mfma_row(short_reg, g) of the last tile for the lanes
+  // of half g = (sl / 4) % 2; those lanes add its log2(n / 128) in units of c1.
+  const int short_slot = (a.nb - 1) % kCoarseSlots;
+  const int short_reg = 4 * (short_slot >> 3) + (short_slot & 3);
+  const float short_lane = g == ((short_slot >> 2) & 1) ? short2 / c1 : 0.0f;
 
   // Table tiles (images written by the tables kernel) are copied verbatim into LDS, one
   // tile ahead, by buffer loads over this bank's images; tiles with no omitted block are
@@ -148,7 +160,13 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
     return k;
   };
 
-  float m = -INFINITY, lsum = 0.0f, gsum = 0.0f;
+  // Running max m2 (log2 units), raised lazily: a tile's probabilities are first taken
+  // against the current m2, and only when a lane's sum of them exceeds kSumCap (or is not
+  // finite, as on the first tile where m2 = -inf) is m2 raised to the true running max and
+  // the tile redone.  Every accepted probability is then <= kSumCap, exact to the type's
+  // precision in fp32 and bf16, and no per-score max is taken on the common path.
+  constexpr float kSumCap = 4096.0f;
+  float m2 = -INFINITY, lsum = 0.0f, gsum = 0.0f;
   f32x16 oacc[NDT];
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) oacc[dt] = f32x16{};
@@ -197,61 +215,69 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
 
     // Lane (g, l32) holds slots mfma_row(rr, g): bits 8 (rr / 4) + 4 g + rr % 4 of the word,
     // the same for the 32 lanes of a half-wave, so each slot's omitted flag is a wave mask
-    // built on the scalar unit.  Kept blocks get -inf (branch-free selects).  The log-count ln 128 common to every full
-    // block is left out of the scores and added to the LSE at the end (softmax, gated share
-    // and output do not depend on it); a short last block gets ln(n / 128) in its own tile.
-    float sc[16];
-    bool gate[16];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int rr = 0; rr < 16; ++rr) {
+    // built on the scalar unit; kept blocks get p = 0 (a select after the exp).  The
+    // log-count ln 128 common to every full block is left out of the scores and added to
+    // the LSE at the end (softmax, gated share and output do not depend on it); a short
+    // last block gets log2(n / 128) in its own tile.
+    auto omitted = [&](int rr) {
       const int sh = 8 * (rr >> 2) + (rr & 3);
-      const bool om = __builtin_amdgcn_inverse_ballot_w64(
+      return __builtin_amdgcn_inverse_ballot_w64(
           (((ow >> sh) & 1u) ? 0x00000000ffffffffull : 0ull) |
           (((ow >> (sh + 4)) & 1u) ? 0xffffffff00000000ull : 0ull));
-      const float quad = wacc[rr];
-      // A kept block's score is -inf, so p = 0 there whatever its gate says.
-      const bool gt = quad * ssq <= thsq;
-      const float v = fmaf(sacc[rr], s32, gt ? quad * half : 0.0f);
-      sc[rr] = om ? v : -INFINITY;
-      gate[rr] = gt;
-    }
-    if (k == last_tile && ln_short != 0.0f) {
+    };
+    // The short last block's log2(n / 128), moved into its q.kbar score (units of c1) so the
+    // loops below stay free of it.
+    if (k == last_tile && short2 != 0.0f) {
+      int sreg = short_reg;
+      asm volatile("" : "+s"(sreg));  // keeps the 16 compares in this rare branch
 #pragma unroll
       for (int rr = 0; rr < 16; ++rr)
-        if (kCoarseSlots * k + mfma_row(rr, g) == a.nb - 1) sc[rr] += ln_short;
+        if (rr == sreg) sacc[rr] += short_lane;
     }
+    float p[16];
+    float part = 0.0f, gpart = 0.0f;
+    // Probabilities against m2: score - m2 = c1 s + (gate ? c2 quad : 0) - m2, the gate
+    // term and -m2 folded into one select.
+    auto probs = [&]() __attribute__((always_inline)) {
+      part = 0.0f;
+      gpart = 0.0f;
 #pragma unroll
-    for (int rr = 0; rr < 16; ++rr) mx = __builtin_elementwise_maximum(mx, sc[rr]);
-    // Lazy running max: moves only when it grows by more than kTailSlack (p stays < 2^8).
-    mx = pair_max(mx);
-    const bool grow = mx > m + kTailSlack;
-    if (__any(grow)) {
-      const float mnew = grow ? mx : m;
-      const float alpha = __builtin_amdgcn_exp2f((m - mnew) * kLog2e);
-      lsum *= alpha;
-      gsum *= alpha;
+      for (int rr = 0; rr < 16; ++rr) {
+        const bool gate = wacc[rr] <= thq;
+        const float tm = gate ? fmaf(wacc[rr], c2, -m2) : -m2;
+        const float e = __builtin_amdgcn_exp2f(fmaf(sacc[rr], c1, tm));
+        p[rr] = omitted(rr) ? e : 0.0f;
+        part += p[rr];
+        gpart += gate ? p[rr] : 0.0f;
+      }
+    };
+    probs();
+    if (__any(!(part <= kSumCap))) {
+      // Raise m2 to the running max over this tile's omitted slots (both lanes of a row).
+      float mx = -INFINITY;
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) oacc[dt] *= alpha;
-      m = mnew;
+      for (int rr = 0; rr < 16; ++rr) {
+        const float sc = fmaf(sacc[rr], c1, wacc[rr] <= thq ? wacc[rr] * c2 : 0.0f);
+        mx = __builtin_elementwise_maximum(mx, omitted(rr) ? sc : -INFINITY);
+      }
+      mx = pair_max(mx);
+      if (mx > m2) {
+        const float alpha = __builtin_amdgcn_exp2f(m2 - mx);
+        lsum *= alpha;
+        gsum *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) oacc[dt] *= alpha;
+        m2 = mx;
+      }
+      probs();
     }
-    const float m_log2 = m * kLog2e;
+    lsum += part;
+    gsum += gpart;
     u32x4 pk[2];
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      unsigned w[4];
-#pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[8 * hh + e], kLog2e, -m_log2));
-        const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[8 * hh + e + 1], kLog2e, -m_log2));
-        lsum += p0;
-        lsum += p1;
-        gsum += gate[8 * hh + e] ? p0 : 0.0f;
-        gsum += gate[8 * hh + e + 1] ? p1 : 0.0f;
-        w[e >> 1] = pack2<T>(p0, p1);
-      }
-      pk[hh] = u32x4{w[0], w[1], w[2], w[3]};
-    }
+    for (int hh = 0; hh < 2; ++hh)
+      pk[hh] = u32x4{pack2<T>(p[8 * hh], p[8 * hh + 1]), pack2<T>(p[8 * hh + 2], p[8 * hh + 3]),
+                     pack2<T>(p[8 * hh + 4], p[8 * hh + 5]), pack2<T>(p[8 * hh + 6], p[8 * hh + 7])};
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
@@ -298,7 +324,7 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
           u32x2{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3])};
     }
   }
-  const float lse = has_tail ? (m + logf(l)) + ln_full : -INFINITY;
+  const float lse = has_tail ? (m2 * kLn2 + logf(l)) + ln_full : -INFINITY;
   if (g == 0) a.gl[ri] = lse;
   if (a.glref != nullptr) {
     const float diff = half_wave_sum(lse - a.glref[ri]);
