@@ -78,6 +78,15 @@ int check_qkv(const char* name, const void* p, int64_t batch, int64_t heads, int
   return RECAP_OK;
 }
 
+// Softmax scale of an attention launch: positive and finite (the kernels' running max is
+// taken over raw scores and scaled afterwards, which needs scale > 0).
+int set_scale(AttnArgs& a, float scale) {
+  REQUIRE(std::isfinite(scale) && scale > 0.0f, "scale must be positive and finite, got %g",
+          (double)scale);
+  a.scale_log2 = scale * kLog2e;
+  return RECAP_OK;
+}
+
 #define CHECK(expr)                 \
   do {                              \
     const int _rc = (expr);         \
@@ -349,6 +358,8 @@ int recap_coarse_tail(const void* q, int dtype, int64_t batch, int64_t heads, in
   CHECK(check_tokens(n_tokens, n_video));
   CHECK(check_qkv("q", q, batch, heads, stride_b, stride_h, stride_n));
   REQUIRE(rowmap && partition && kbar && vbar && w && u_t && cvk_t && go && gl, "NULL pointer");
+  REQUIRE(std::isfinite(scale) && scale > 0.0f, "scale must be positive and finite");
+  REQUIRE(theta >= 0.0f, "theta must be non-negative");
   REQUIRE(aligned16(kbar) && aligned16(vbar) && aligned16(w) && aligned16(u_t) && aligned16(cvk_t) && aligned16(go),
           "tables must be 16-byte aligned");
   REQUIRE(glref == nullptr || drift_partial != nullptr, "glref needs drift_partial");
@@ -410,7 +421,7 @@ int recap_block_sparse_attn(const void* q, int dtype, int64_t batch, int64_t hea
   REQUIRE(kernel_mask && head_out && head_lse, "NULL mask or output");
   REQUIRE(aligned16(head_out), "head_out must be 16-byte aligned");
   a.kmask = kernel_mask; a.ds = a.tb;
-  a.scale_log2 = scale * kLog2e;
+  CHECK(set_scale(a, scale));
   a.head_out = head_out; a.head_lse = head_lse;
   return hip_status(run_attention(a, dtype, (int)dim, kModeHead, as_stream(stream)), "attention launch");
 }
@@ -426,7 +437,7 @@ int recap_dense_attn(const void* q, int dtype, int64_t batch, int64_t heads, int
   CHECK(check_qkv("out", out, batch, heads, out_stride_b, out_stride_h, out_stride_n));
   REQUIRE(lse != nullptr, "lse is NULL");
   a.ds = a.tb;
-  a.scale_log2 = scale * kLog2e;
+  CHECK(set_scale(a, scale));
   a.out = static_cast<uint16_t*>(out); a.osB = out_stride_b; a.osH = out_stride_h; a.osN = out_stride_n;
   a.lse_native = lse;
   return hip_status(run_attention(a, dtype, (int)dim, kModeDense, as_stream(stream)), "attention launch");
@@ -446,7 +457,7 @@ int recap_dense_head_attn(const void* q, int dtype, int64_t batch, int64_t heads
   REQUIRE(lse != nullptr && head_out != nullptr && head_lse != nullptr, "lse/head_out/head_lse NULL");
   a.kmask = kernel_mask;
   a.ds = a.tb;  // every query block walks all tb blocks: no long items to start first
-  a.scale_log2 = scale * kLog2e;
+  CHECK(set_scale(a, scale));
   a.out = static_cast<uint16_t*>(out); a.osB = out_stride_b; a.osH = out_stride_h; a.osN = out_stride_n;
   a.lse_native = lse;
   a.head_out = head_out; a.head_lse = head_lse;
@@ -471,7 +482,7 @@ int recap_sparse_merge_attn(const void* q, int dtype, int64_t batch, int64_t hea
     REQUIRE(alpha_override >= 0.0f || (glref && center), "drift weight needs glref and center");
   }
   a.kmask = kernel_mask;
-  a.scale_log2 = scale * kLog2e;
+  CHECK(set_scale(a, scale));
   a.out = static_cast<uint16_t*>(out); a.osB = out_stride_b; a.osH = out_stride_h; a.osN = out_stride_n;
   a.go = static_cast<const uint16_t*>(go); a.gl = gl; a.det = static_cast<const uint16_t*>(det);
   a.dl = dl; a.glref = glref; a.center = center;

@@ -262,11 +262,13 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
   }
   tile_barrier();
 
-  float m[kGroups], lsum[kGroups];
+  float m[kGroups], mraw[kGroups], lsum[kGroups];
+  const float inv_scale_log2 = 1.0f / a.scale_log2;
   f32x16 oacc[kGroups][NDT];
 #pragma unroll
   for (int q = 0; q < kGroups; ++q) {
     m[q] = -INFINITY;
+    mraw[q] = -INFINITY;
     lsum[q] = 0.0f;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) oacc[q][dt] = f32x16{};
@@ -296,18 +298,20 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
         for (int rr = 0; rr < 16; ++rr)
           if (32 * kt + mfma_row(rr, g) >= limit) s[q][kt][rr] = -INFINITY;
   };
-  // Lazy running-max update of group q from a per-lane candidate: moves only when the row
-  // max grows by more than kRescaleSlack, rescaling O and l.
+  // Lazy running-max update of group q from a per-lane candidate raw score: moves only when
+  // the row max grows by more than kRescaleSlack, rescaling O and l.  The test is on raw
+  // scores against mraw = (m + slack) / (scale log2 e), kept with m (scale > 0).
   auto update_max = [&](int q, float mx) {
-    const float mt = pair_max(mx) * a.scale_log2;
-    const bool grow = mt > m[q] + kRescaleSlack;
+    const float pm = pair_max(mx);
+    const bool grow = pm > mraw[q];
     if (__any(grow)) {
-      const float mnew = grow ? mt : m[q];
+      const float mnew = grow ? pm * a.scale_log2 : m[q];
       const float alpha = __builtin_amdgcn_exp2f(m[q] - mnew);
       lsum[q] *= alpha;
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) oacc[q][dt] *= alpha;
       m[q] = mnew;
+      mraw[q] = (mnew + kRescaleSlack) * inv_scale_log2;
     }
   };
   auto row_max = [&](f32x16 (&s)[kGroups][2]) {
@@ -400,7 +404,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
               nxt[q][kt2][rr] = s0;
               nxt[q][kt2][rr + 1] = s1;
             }
-            mx[q] = __builtin_elementwise_maximum(mx[q], __builtin_elementwise_maximum(s0, s1));
+            mx[q] = fmaxf(fmaxf(mx[q], s0), s1);  // one v_max3_f32 per pair
           }
         }
       }

@@ -69,6 +69,16 @@ def test_argument_validation_before_launch():
     with pytest.raises(ValueError, match="kernel blocks"):
         _lib.call("recap_dense_attn", 16, _lib.RECAP_BF16, 1, 1, 64, 0, 0, 64, 16, 16, 16,
                   2049 * 128, 0.125, 16, 0, 0, 64, 16, None)
+    for bad in (0.0, -0.125, float("inf"), float("nan")):
+        with pytest.raises(ValueError, match="scale"):
+            _lib.call("recap_dense_attn", 16, _lib.RECAP_BF16, 1, 1, 64, 0, 0, 64, 16, 16, 16,
+                      256, bad, 16, 0, 0, 64, 16, None)
+        with pytest.raises(ValueError, match="scale"):
+            _lib.call("recap_block_sparse_attn", 16, _lib.RECAP_BF16, 1, 1, 64, 0, 0, 64, 16, 16,
+                      16, 16, 256, bad, 16, 16, None)
+    with pytest.raises(ValueError, match="theta"):
+        _lib.call("recap_coarse_tail", 16, _lib.RECAP_BF16, 1, 1, 64, 0, 0, 64, 16, 16, 16, 16,
+                  16, 16, 16, 256, 256, 0.125, -1.0, None, 16, 16, 16, None)
     with pytest.raises(ValueError, match="matrix order"):
         _lib.call("recap_symmetric_eigen", 16, 2, 129, 16, 16, None)
     with pytest.raises(ValueError, match="matrix order"):
