@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define RECAP_ABI_VERSION 1
+#define RECAP_ABI_VERSION 2
 
 enum { RECAP_OK = 0, RECAP_EINVAL = 1, RECAP_EUNSUPPORTED = 2, RECAP_EHIP = 3 };
 enum { RECAP_F16 = 1, RECAP_BF16 = 2 };
@@ -131,16 +131,24 @@ int recap_partial_reduce(const float* partial, int64_t banks, int64_t groups, in
 int recap_symmetric_eigen(const float* a, int64_t batch, int64_t n, float* eigenvalues,
                           float* eigenvectors, void* stream);
 
-/* Query-type tables of the coarse tail: w = fold_rank(variance, rank) (columns in swap23
- * order), kbar, vbar, each written as tile images of 32 key blocks, [banks, ceil(nb/32)*32,
- * dim] elements (rows past nb zero): kbar and w tiles in the packed K-tile layout, vbar
- * tiles transposed ([dim][32 positions], position p holding block swap23(p)), so the
- * coarse tail copies a tile verbatim into LDS.
+/* Query-type tables of the coarse tail: w = fold_rank(variance, rank), kbar, vbar, each
+ * written as tile images of 32 key blocks, [banks, ceil(nb/32)*32, width] elements (rows
+ * past nb zero), width = dim for kbar and vbar and recap_coarse_w_width() for w.  kbar
+ * tiles are in the packed K-tile layout, vbar tiles transposed ([dim][32 positions],
+ * position p holding block swap23(p)), so the coarse tail copies a tile verbatim into LDS.
+ * w is either the full fold_rank row in the K-tile layout (columns in swap23 order) or,
+ * when the fold leaves few distinct values (bf16, 1 <= rank <= 13), the 16 features
+ * [w_0 .. w_{rank-1}, rho, rho, rho, 0 ...] with rho the mean of the folded columns.
  * Replaces fold_rank (recap/sparse/closure.py:96-104) and the casts of
  * recap/kernels/coarse_tail.py:238-241. */
 int recap_coarse_tables(const float* variance, const float* k_means, const float* v_means,
                         int dtype, int64_t banks, int64_t n_blocks, int64_t dim, int64_t rank,
                         void* w, void* kbar, void* vbar, void* stream);
+
+/* Columns of the w table for (dtype, dim, rank): 16 in the folded form, else dim; -1 for
+ * invalid arguments.  Host only.  Sizes the w buffer of recap_coarse_tables (no
+ * counterpart in the reference, whose w keeps dim columns). */
+int64_t recap_coarse_w_width(int dtype, int64_t dim, int64_t rank);
 
 /* Basis tables [banks, dim, dim]: U^T split hi/lo (closure statistics), U^T and C_vk in
  * the query type (coarse tail).  Any output may be NULL; cvk may be NULL if cvk_t is.
@@ -152,7 +160,8 @@ int recap_basis_tables(const float* basis, const float* cvk, int dtype, int64_t 
 
 /* Corrected coarse tail for the R refined rows: go [banks, R, dim] (query type),
  * gl [banks, R] fp32; with glref [banks, R] also drift_partial [banks, R/128].  kbar, vbar
- * and w are the tile images written by recap_coarse_tables.
+ * and w are the tile images written by recap_coarse_tables with the same dtype, dim and
+ * rank (the closure rank of fold_rank, which selects the w layout).
  * Replaces coarse_tail_attention + _coarse_tail_kernel (recap/kernels/coarse_tail.py:
  * 35-312), build_coarse_tail_plan (recap/sparse/planner.py:11-38), rotated_query_square
  * and value_drift (recap/sparse/closure.py:84-93) and coarse_tail_apply
@@ -162,8 +171,8 @@ int recap_coarse_tail(const void* q, int dtype, int64_t batch, int64_t heads, in
                       const int32_t* rowmap, const uint8_t* partition, const void* kbar,
                       const void* vbar, const void* w, const void* u_t, const void* cvk_t,
                       int64_t n_tokens, int64_t n_video, float scale, float theta,
-                      const float* glref, void* go, float* gl, float* drift_partial,
-                      void* stream);
+                      int64_t rank, const float* glref, void* go, float* gl,
+                      float* drift_partial, void* stream);
 
 /* center[b] = sum(drift_partial[b, :]) / R.
  * Replaces _drift_center, recap/operator.py:148-150. */

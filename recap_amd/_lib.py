@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "librecap_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 RECAP_OK, RECAP_EINVAL, RECAP_EUNSUPPORTED, RECAP_EHIP = 0, 1, 2, 3
 RECAP_F16, RECAP_BF16 = 1, 2
@@ -42,8 +42,9 @@ SIGNATURES: dict[str, tuple] = {
     "recap_symmetric_eigen": (_I, [_P, _I64, _I64, _P, _P, _P]),
     "recap_coarse_tables": (_I, [_P, _P, _P, _I, _I64, _I64, _I64, _I64, _P, _P, _P, _P]),
     "recap_basis_tables": (_I, [_P, _P, _I, _I64, _I64, _P, _P, _P, _P, _P]),
+    "recap_coarse_w_width": (_I64, [_I, _I64, _I64]),
     "recap_coarse_tail": (_I, [_P, _I, _I64, _I64, _I64, *_STRIDES, _P, _P, _P, _P, _P, _P, _P,
-                               _I64, _I64, _F, _F, _P, _P, _P, _P, _P]),
+                               _I64, _I64, _F, _F, _I64, _P, _P, _P, _P, _P]),
     "recap_drift_center": (_I, [_P, _I64, _I64, _P, _P]),
     "recap_block_sparse_attn": (_I, [_P, _I, _I64, _I64, _I64, *_STRIDES, _P, _P, _P, _P, _I64,
                                      _F, _P, _P, _P]),

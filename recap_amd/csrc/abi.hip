@@ -335,6 +335,11 @@ int recap_coarse_tables(const float* variance, const float* k_means, const float
   return hip_status(run_tables(a, dtype, as_stream(stream)), "coarse_tables launch");
 }
 
+int64_t recap_coarse_w_width(int dtype, int64_t dim, int64_t rank) {
+  if (check_common(dtype, dim) != RECAP_OK || rank < 0) return -1;
+  return coarse_folded(dtype, (int)dim, (int)rank) ? kFoldCols : dim;
+}
+
 int recap_basis_tables(const float* basis, const float* cvk, int dtype, int64_t banks,
                        int64_t dim, void* u_hi_t, void* u_lo_t, void* u_t, void* cvk_t,
                        void* stream) {
@@ -352,14 +357,15 @@ int recap_coarse_tail(const void* q, int dtype, int64_t batch, int64_t heads, in
                       const int32_t* rowmap, const uint8_t* partition, const void* kbar,
                       const void* vbar, const void* w, const void* u_t, const void* cvk_t,
                       int64_t n_tokens, int64_t n_video, float scale, float theta,
-                      const float* glref, void* go, float* gl, float* drift_partial,
-                      void* stream) {
+                      int64_t rank, const float* glref, void* go, float* gl,
+                      float* drift_partial, void* stream) {
   CHECK(check_common(dtype, dim));
   CHECK(check_tokens(n_tokens, n_video));
   CHECK(check_qkv("q", q, batch, heads, stride_b, stride_h, stride_n));
   REQUIRE(rowmap && partition && kbar && vbar && w && u_t && cvk_t && go && gl, "NULL pointer");
   REQUIRE(std::isfinite(scale) && scale > 0.0f, "scale must be positive and finite");
   REQUIRE(theta >= 0.0f, "theta must be non-negative");
+  REQUIRE(rank >= 0 && rank <= dim, "rank %lld outside [0, dim]", (long long)rank);
   REQUIRE(aligned16(kbar) && aligned16(vbar) && aligned16(w) && aligned16(u_t) && aligned16(cvk_t) && aligned16(go),
           "tables must be 16-byte aligned");
   REQUIRE(glref == nullptr || drift_partial != nullptr, "glref needs drift_partial");
@@ -374,7 +380,7 @@ int recap_coarse_tail(const void* q, int dtype, int64_t batch, int64_t heads, in
   a.u_t = static_cast<const uint16_t*>(u_t); a.cvk = static_cast<const uint16_t*>(cvk_t);
   a.heads = (int)heads; a.banks = (int)(batch * heads); a.nb = (int)g.nb;
   a.n_video = (int)n_video; a.rows = (int)g.rows; a.qtiles = (int)(g.rows / kBlock);
-  a.scale = scale; a.theta = theta; a.glref = glref;
+  a.scale = scale; a.theta = theta; a.rank = (int)rank; a.glref = glref;
   a.go = static_cast<uint16_t*>(go); a.gl = gl; a.drift_part = drift_partial;
   return hip_status(run_coarse(a, dtype, (int)dim, as_stream(stream)), "coarse_tail launch");
 }

@@ -283,8 +283,10 @@ hipError_t run_partial_reduce(const float* part, int banks, int groups, int elem
 
 // One workgroup per padded table row (bank, j), j < ntiles * 32: fold_rank of the rotated
 // variance (recap/sparse/closure.py:96-104), then w, kbar, vbar rounded to the query type
-// and written into their tile images (rows j >= nb are zero).
-template <class T, int D>
+// and written into their tile images (rows j >= nb are zero).  FOLD writes w as the
+// kFoldCols-feature row [w_0 .. w_{r-1}, rho, rho, rho, 0 ...] (natural order), 32 rows of
+// 32 bytes per tile.
+template <class T, int D, bool FOLD>
 __global__ __launch_bounds__(128) void tables_kernel(TablesArgs a) {
   using G = TileGeom<D>;
   __shared__ float red[128];
@@ -310,10 +312,18 @@ __global__ __launch_bounds__(128) void tables_kernel(TablesArgs a) {
   if (t < D) {
     const int64_t tile_base = ((int64_t)bank * ntiles + tile) * kCoarseSlots * D * 2;  // bytes
     const int koff = G::k_off(slot, t >> 3) + ((t & 7) << 1);
-    const uint16_t wv = real ? T::from_f(vals[swap23(t)]) : (uint16_t)0;
     const uint16_t kv = real ? T::from_f(a.kmean[row * D + t]) : (uint16_t)0;
     const uint16_t vv = real ? T::from_f(a.vmean[row * D + t]) : (uint16_t)0;
-    *reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(a.w_t) + tile_base + koff) = wv;
+    if constexpr (FOLD) {
+      if (t < kFoldCols) {
+        const float f = t < a.rank ? vals[t] : (t < a.rank + 3 ? residual : 0.0f);
+        a.w_t[((int64_t)bank * ntiles * kCoarseSlots + j) * kFoldCols + t] =
+            real ? T::from_f(f) : (uint16_t)0;
+      }
+    } else {
+      const uint16_t wv = real ? T::from_f(vals[swap23(t)]) : (uint16_t)0;
+      *reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(a.w_t) + tile_base + koff) = wv;
+    }
     *reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(a.kbar_t) + tile_base + koff) = kv;
     *reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(a.vbar_t) + tile_base +
                                  coarse_vt_off(t, swap23(slot))) = vv;
@@ -323,12 +333,18 @@ __global__ __launch_bounds__(128) void tables_kernel(TablesArgs a) {
 hipError_t run_tables(const TablesArgs& a, int dtype, hipStream_t s) {
   const int ntiles = (a.nb + kCoarseSlots - 1) / kCoarseSlots;
   const dim3 grid((unsigned)(a.banks * ntiles * kCoarseSlots)), block(128);
+  const bool fold = coarse_folded(dtype, a.dim, a.rank);
   if (dtype == BF16::code) {
-    if (a.dim == 128) hipLaunchKernelGGL((tables_kernel<BF16, 128>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((tables_kernel<BF16, 64>), grid, block, 0, s, a);
+    if (a.dim == 128) {
+      if (fold) hipLaunchKernelGGL((tables_kernel<BF16, 128, true>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((tables_kernel<BF16, 128, false>), grid, block, 0, s, a);
+    } else {
+      if (fold) hipLaunchKernelGGL((tables_kernel<BF16, 64, true>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((tables_kernel<BF16, 64, false>), grid, block, 0, s, a);
+    }
   } else {
-    if (a.dim == 128) hipLaunchKernelGGL((tables_kernel<F16, 128>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((tables_kernel<F16, 64>), grid, block, 0, s, a);
+    if (a.dim == 128) hipLaunchKernelGGL((tables_kernel<F16, 128, false>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((tables_kernel<F16, 64, false>), grid, block, 0, s, a);
   }
   return hipGetLastError();
 }

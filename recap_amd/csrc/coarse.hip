@@ -23,16 +23,19 @@ namespace recap {
 
 constexpr int kMaxVideoBlocks = 4096;
 
-template <class T, int D>
+template <class T, int D, bool FOLD>
 __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
 #pragma clang fp contract(off)
   using G = TileGeom<D>;
   constexpr int NS = D / 16, NDT = D / 32, NCH = D / 8;
   constexpr int kMatBytes = D * D * 2;
-  constexpr int kTabBytes = kCoarseSlots * D * 2;  // one table tile image
-  constexpr int kStage = 3 * kTabBytes;            // the kbar, w, vbar tiles of one tile
+  constexpr int kTabBytes = kCoarseSlots * D * 2;  // one kbar or vbar tile image
+  // One w tile image: the folded features (32 rows of kFoldCols) or a full K-tile layout.
+  constexpr int kWBytes = FOLD ? kCoarseSlots * kFoldCols * 2 : kTabBytes;
+  constexpr int kStage = 2 * kTabBytes + kWBytes;  // kbar, vbar, w of one tile
   constexpr int NDMA = kTabBytes / 4096;           // 16-byte copies per thread per image
   static_assert(2 * kStage >= kMatBytes, "a staged D x D matrix spans both stages");
+  static_assert(!FOLD || kWBytes == 1024, "a folded w tile is 4 bytes per thread");
   // Two tile stages in separate arrays, each access naming one of them at compile time: the
   // compiler can then tell that reads of one stage do not touch the copies filling the other,
   // and does not wait for those copies first.  A staged D x D matrix (U^T, C_vk) keeps rows
@@ -42,6 +45,7 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
   __shared__ __attribute__((aligned(16))) char st1[kStage];
   __shared__ unsigned omit[kMaxVideoBlocks / kCoarseSlots];
   __shared__ float wsum[4];
+  __shared__ float feat[FOLD ? 4 * 32 * kFoldCols : 1];  // folded qsq features per row
 
   const int t = threadIdx.x, lane = t & 63, g = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -89,25 +93,63 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
   }
   __syncthreads();
 
-  // qsq in the B-operand layout of the quadratic form.
-  u32x4 qsq_pk[NDT][2];
+  // qsq = (U^T q)^2 in the query type (rotated value rounded, then its square rounded):
+  // lane (g, l32) holds dims 32 ot + mfma_row(rr, g) of its row.  Full form: qsq in the
+  // B-operand layout of the quadratic form (dims in swap23 order, as the w table's
+  // columns).  Folded form: the kFoldCols features [qsq_0 .. qsq_{r-1}, T_hi, T_mid, T_lo,
+  // 0 ...] as one B operand, gathered through LDS (lane (g, l32) holds features 8g .. 8g+7).
+  constexpr int kQsqRegs = FOLD ? 1 : NDT * 2;
+  u32x4 qsq_pk[kQsqRegs];
+  float* frow = feat + (wave * 32 + l32) * kFoldCols;
+  if constexpr (FOLD) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) frow[8 * g + e] = 0.0f;
+    __syncthreads();
+  }
+  float tail = 0.0f;
 #pragma unroll
   for (int ot = 0; ot < NDT; ++ot) {
     f32x16 acc = f32x16{};
 #pragma unroll
     for (int s = 0; s < NS; ++s)
       acc = T::mfma32(matrix_frag(ot, 2 * s + g), qreg[s], acc);
+    float sq[16];
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      unsigned w[4];
-#pragma unroll
-      for (int e = 0; e < 8; e += 2) {
-        const float x0 = T::to_f(T::from_f(acc[8 * hh + e]));
-        const float x1 = T::to_f(T::from_f(acc[8 * hh + e + 1]));
-        w[e >> 1] = pack2<T>(x0 * x0, x1 * x1);
-      }
-      qsq_pk[ot][hh] = u32x4{w[0], w[1], w[2], w[3]};
+    for (int rr = 0; rr < 16; ++rr) {
+      const float x = T::to_f(T::from_f(acc[rr]));
+      sq[rr] = T::to_f(T::from_f(x * x));
     }
+    if constexpr (FOLD) {
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) {
+        const int c = 32 * ot + mfma_row(rr, g);
+        if (c < a.rank) frow[c] = sq[rr];
+        else tail += sq[rr];
+      }
+    } else {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+        qsq_pk[2 * ot + hh] = u32x4{pack2<T>(sq[8 * hh], sq[8 * hh + 1]),
+                                    pack2<T>(sq[8 * hh + 2], sq[8 * hh + 3]),
+                                    pack2<T>(sq[8 * hh + 4], sq[8 * hh + 5]),
+                                    pack2<T>(sq[8 * hh + 6], sq[8 * hh + 7])};
+    }
+  }
+  if constexpr (FOLD) {
+    // T = sum_{c>=r} qsq_c over both lanes of the row, split into three bf16 parts.
+    const float total = pair_sum(tail);
+    const float hi = T::to_f(T::from_f(total));
+    const float mid = T::to_f(T::from_f(total - hi));
+    const float lo = T::to_f(T::from_f((total - hi) - mid));
+    if (g == 0) {
+      frow[a.rank] = hi;
+      frow[a.rank + 1] = mid;
+      frow[a.rank + 2] = lo;
+    }
+    __syncthreads();
+    const float* f8 = frow + 8 * g;
+    qsq_pk[0] = u32x4{pack2<T>(f8[0], f8[1]), pack2<T>(f8[2], f8[3]), pack2<T>(f8[4], f8[5]),
+                      pack2<T>(f8[6], f8[7])};
   }
   __syncthreads();  // the table tiles reuse the U^T staging area
 
@@ -136,12 +178,14 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
   // Table tiles (images written by the tables kernel) are copied verbatim into LDS, one
   // tile ahead, by buffer loads over this bank's images; tiles with no omitted block are
   // skipped.
+  // Stage layout: kbar image, vbar image, w image.
   const int bank_tab = ntiles * kTabBytes;
   const int64_t tab_elems = (int64_t)bank * ntiles * kCoarseSlots * D;
+  const int64_t w_elems = (int64_t)bank * ntiles * (kWBytes / 2);
   const __amdgpu_buffer_rsrc_t krs =
       __builtin_amdgcn_make_buffer_rsrc((void*)(a.kbar + tab_elems), 0, bank_tab, kBufferRsrcWord3);
-  const __amdgpu_buffer_rsrc_t wrs =
-      __builtin_amdgcn_make_buffer_rsrc((void*)(a.w + tab_elems), 0, bank_tab, kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.w + w_elems), 0, ntiles * kWBytes, kBufferRsrcWord3);
   const __amdgpu_buffer_rsrc_t vrs =
       __builtin_amdgcn_make_buffer_rsrc((void*)(a.vbar + tab_elems), 0, bank_tab, kBufferRsrcWord3);
   auto copy_tile = [&](int k, char* dst) {
@@ -150,8 +194,14 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
     for (int i = 0; i < NDMA; ++i) {
       const int lo = 4096 * i + 1024 * wave, vo = 4096 * i + 16 * t;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void*)(dst + lo), 16, vo, off, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_void*)(dst + kTabBytes + lo), 16, vo, off, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void*)(dst + 2 * kTabBytes + lo), 16, vo, off, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void*)(dst + kTabBytes + lo), 16, vo, off, 0, 0);
+      if constexpr (!FOLD)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_void*)(dst + 2 * kTabBytes + lo), 16, vo, off, 0, 0);
+    }
+    if constexpr (FOLD) {  // 1 KB: 4 bytes per thread
+      const int woff = __builtin_amdgcn_readfirstlane(k * kWBytes);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_void*)(dst + 2 * kTabBytes + 256 * wave), 4,
+                                               4 * t, woff, 0, 0);
     }
   };
   auto next_tile = [&](int k) {
@@ -182,28 +232,42 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
     if (kn < ntiles) copy_tile(kn, nxt);
 
     const char* kb_lds = cur;
-    const char* w_lds = kb_lds + kTabBytes;
-    const char* vt_lds = kb_lds + 2 * kTabBytes;
+    const char* vt_lds = kb_lds + kTabBytes;
+    const char* w_lds = kb_lds + 2 * kTabBytes;
     const unsigned ow = __builtin_amdgcn_readfirstlane(omit[k]);
     // The two independent chains s = q.kbar and quad = qsq.w (NS MFMAs each, chunk 2 s + g
     // of both tiles) interleaved, each slice reading its fragments two slices ahead, so no
     // MFMA waits on an LDS read issued just before it.
     f32x16 sacc = f32x16{}, wacc = f32x16{};
-    u32x4 kf[3], wf[3];
+    if constexpr (FOLD) {
+      // quad = qsq'.w' over the kFoldCols folded features: one MFMA; then the q.kbar chain.
+      wacc = T::mfma32(lds_load16(w_lds, 32 * l32 + 16 * g), qsq_pk[0], wacc);
+      u32x4 kf[3];
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      kf[s] = lds_load16(kb_lds, G::k_off(l32, 2 * s + g));
-      wf[s] = lds_load16(w_lds, G::k_off(l32, 2 * s + g));
-    }
+      for (int s = 0; s < 2; ++s) kf[s] = lds_load16(kb_lds, G::k_off(l32, 2 * s + g));
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      if (s + 2 < NS) {
-        kf[(s + 2) % 3] = lds_load16(kb_lds, G::k_off(l32, 2 * (s + 2) + g));
-        wf[(s + 2) % 3] = lds_load16(w_lds, G::k_off(l32, 2 * (s + 2) + g));
+      for (int s = 0; s < NS; ++s) {
+        if (s + 2 < NS) kf[(s + 2) % 3] = lds_load16(kb_lds, G::k_off(l32, 2 * (s + 2) + g));
+        sacc = T::mfma32(kf[s % 3], qreg[s], sacc);
+        __builtin_amdgcn_sched_barrier(0);
       }
-      sacc = T::mfma32(kf[s % 3], qreg[s], sacc);
-      wacc = T::mfma32(wf[s % 3], qsq_pk[s >> 1][s & 1], wacc);
-      __builtin_amdgcn_sched_barrier(0);
+    } else {
+      u32x4 kf[3], wf[3];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        kf[s] = lds_load16(kb_lds, G::k_off(l32, 2 * s + g));
+        wf[s] = lds_load16(w_lds, G::k_off(l32, 2 * s + g));
+      }
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        if (s + 2 < NS) {
+          kf[(s + 2) % 3] = lds_load16(kb_lds, G::k_off(l32, 2 * (s + 2) + g));
+          wf[(s + 2) % 3] = lds_load16(w_lds, G::k_off(l32, 2 * (s + 2) + g));
+        }
+        sacc = T::mfma32(kf[s % 3], qreg[s], sacc);
+        wacc = T::mfma32(wf[s % 3], qsq_pk[s], wacc);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
     // V-bar fragments of the PV product, read now so they are in registers after the softmax.
     u32x4 vf[NDT][2];
@@ -334,15 +398,18 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
   }
 }
 
-template <class T, int D>
+template <class T, int D, bool FOLD>
 static hipError_t launch_coarse(const CoarseArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((coarse_kernel<T, D>), dim3((unsigned)(a.banks * a.qtiles)), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((coarse_kernel<T, D, FOLD>), dim3((unsigned)(a.banks * a.qtiles)), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
 hipError_t run_coarse(const CoarseArgs& a, int dtype, int dim, hipStream_t s) {
-  if (dtype == BF16::code) return dim == 128 ? launch_coarse<BF16, 128>(a, s) : launch_coarse<BF16, 64>(a, s);
-  return dim == 128 ? launch_coarse<F16, 128>(a, s) : launch_coarse<F16, 64>(a, s);
+  if (coarse_folded(dtype, dim, a.rank))
+    return dim == 128 ? launch_coarse<BF16, 128, true>(a, s) : launch_coarse<BF16, 64, true>(a, s);
+  if (dtype == BF16::code)
+    return dim == 128 ? launch_coarse<BF16, 128, false>(a, s) : launch_coarse<BF16, 64, false>(a, s);
+  return dim == 128 ? launch_coarse<F16, 128, false>(a, s) : launch_coarse<F16, 64, false>(a, s);
 }
 
 // Per-bank drift centre c = sum(partials) / rows (recap/operator.py:148-150).

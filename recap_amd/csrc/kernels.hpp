@@ -49,6 +49,19 @@ struct TablesArgs {
   const float* var; const float* kmean; const float* vmean; int banks, nb, dim, rank;
   uint16_t* w_t; uint16_t* kbar_t; uint16_t* vbar_t;   // element type of the query
 };
+
+// Folded w table of the coarse tail.  fold_rank leaves w with r + 1 distinct values per
+// block (the r leading variances, then one mean rho in every other column), so
+// qsq.w = sum_{c<r} qsq_c w_c + rho * T with T = sum_{c>=r} qsq_c.  With T split into three
+// bf16 parts (exact to fp32), that is a dot product over kFoldCols = 16 features
+// [qsq_0 .. qsq_{r-1}, T_hi, T_mid, T_lo, 0 ...] . [w_0 .. w_{r-1}, rho, rho, rho, 0 ...]:
+// one 32x32x16 MFMA per 32-block tile instead of dim / 16.  bf16 only (its exponent range
+// holds T; fp16 could overflow), 1 <= r <= 13 and r < dim; otherwise the table keeps dim
+// columns and the kernel its full dot product.
+constexpr int kFoldCols = 16;
+inline bool coarse_folded(int dtype, int dim, int rank) {
+  return dtype == BF16::code && rank >= 1 && rank + 3 <= kFoldCols && rank < dim;
+}
 hipError_t run_tables(const TablesArgs& a, int dtype, hipStream_t s);
 struct BasisArgs {
   const float* basis; const float* cvk; int banks, dim;
@@ -70,7 +83,7 @@ struct CoarseArgs {
   const int32_t* rowmap; const uint8_t* partition;
   const uint16_t* kbar; const uint16_t* vbar; const uint16_t* w;   // [bank][nb][D]
   const uint16_t* u_t; const uint16_t* cvk;                        // [bank][D][D]
-  int heads, banks, nb, n_video, rows, qtiles;
+  int heads, banks, nb, n_video, rows, qtiles, rank;
   float scale, theta;
   const float* glref;                  // [bank][rows] or null
   uint16_t* go; float* gl;             // [bank][rows][D], [bank][rows]

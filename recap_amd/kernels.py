@@ -286,12 +286,16 @@ COARSE_SLOTS = 32  # key blocks per coarse-tail table tile
 
 
 def coarse_tables(var: torch.Tensor, kv: PackedKV, rank: int):
-    """w, kbar, vbar as tile images [banks, ceil(nb/32)*32, d] (see recap_coarse_tables)."""
+    """w, kbar, vbar as tile images [banks, ceil(nb/32)*32, width] (see recap_coarse_tables;
+    w is [.., 16] in the folded form)."""
     var = var.to(torch.float32).contiguous()
     banks, nb, d = var.shape
     padded = -(-nb // COARSE_SLOTS) * COARSE_SLOTS
-    mk = lambda: torch.empty(banks, padded, d, dtype=kv.dtype, device=var.device)  # noqa: E731
-    w, kbar, vbar = mk(), mk(), mk()
+    width = int(_lib.load().recap_coarse_w_width(dtype_code(kv.dtype), d, int(rank)))
+    if width < 0:
+        raise ValueError(f"coarse_tables: invalid dtype/dim/rank ({kv.dtype}, {d}, {rank})")
+    mk = lambda c: torch.empty(banks, padded, c, dtype=kv.dtype, device=var.device)  # noqa: E731
+    w, kbar, vbar = mk(width), mk(d), mk(d)
     call("recap_coarse_tables", var.data_ptr(), kv.k_means.data_ptr(), kv.v_means.data_ptr(),
          dtype_code(kv.dtype), banks, nb, d, int(rank), w.data_ptr(), kbar.data_ptr(),
          vbar.data_ptr(), _stream())
@@ -300,7 +304,8 @@ def coarse_tables(var: torch.Tensor, kv: PackedKV, rank: int):
 
 def coarse_tail(q: torch.Tensor, rowmap: torch.Tensor, partition: torch.Tensor, geo: Geometry,
                 tables: dict, scale: float, theta: float, glref: torch.Tensor | None = None):
-    """(go [banks, R, d], gl [banks, R], drift partial [banks, R/128] or None)."""
+    """(go [banks, R, d], gl [banks, R], drift partial [banks, R/128] or None).  `tables`
+    holds the coarse tables and the closure rank they were built with (key "rank")."""
     b, h, n, d = q.shape
     banks = b * h
     partition = partition.contiguous()
@@ -313,7 +318,8 @@ def coarse_tail(q: torch.Tensor, rowmap: torch.Tensor, partition: torch.Tensor, 
     call("recap_coarse_tail", *_qkv_args(q), rowmap.data_ptr(), partition.data_ptr(),
          tables["kbar"].data_ptr(), tables["vbar"].data_ptr(), tables["w"].data_ptr(),
          tables["u_t"].data_ptr(), tables["cvk_t"].data_ptr(), n, geo.n_video, float(scale),
-         float(theta), _p(glref), go.data_ptr(), gl.data_ptr(), _p(part), _stream())
+         float(theta), int(tables["rank"]), _p(glref), go.data_ptr(), gl.data_ptr(), _p(part),
+         _stream())
     return go, gl, part
 
 

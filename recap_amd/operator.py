@@ -79,9 +79,10 @@ class SparseAttention:
             var, cvk, _ = K.closure_stats(kv, geo, _lib.CLOSURE_ROT | _lib.CLOSURE_CVK,
                                           self._tables.u_hi_t, self._tables.u_lo_t)
         cvk_t = K.basis_tables(None, cvk, dtype, cvk_table=True).cvk_t
-        w, kbar, vbar = K.coarse_tables(var, kv, int(self.config.closure_rank))
+        rank = int(self.config.closure_rank)
+        w, kbar, vbar = K.coarse_tables(var, kv, rank)
         return {"w": w, "kbar": kbar, "vbar": vbar, "u_t": self._tables.u_t, "cvk_t": cvk_t,
-                "variance": var, "cvk": cvk}
+                "rank": rank, "variance": var, "cvk": cvk}
 
     def coarse_tail_apply(self, q, rowmap, context, partition, geo, scale, glref=None):
         """Coarse tail over the omitted blocks (recap/sparse/attention.py:204-231)."""

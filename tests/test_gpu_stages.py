@@ -216,10 +216,13 @@ def test_closure_statistics(cuda, name):
     assert rel < 1e-3
 
 
-@pytest.mark.parametrize("name", ["tiny", "text-first-ragged", "text-last-d128",
-                                  "video-ragged-d128"])
-def test_coarse_tail(cuda, name):
-    """The coarse kernel against the oracle fed with the same closure statistics."""
+@pytest.mark.parametrize("name,rank", [("tiny", 4), ("text-first-ragged", 4),
+                                       ("text-last-d128", 4), ("video-ragged-d128", 4),
+                                       ("text-last-d128", 0), ("text-last-d128", 13),
+                                       ("video-ragged-d128", 20)])
+def test_coarse_tail(cuda, name, rank):
+    """The coarse kernel against the oracle fed with the same closure statistics.  Ranks
+    1-13 take the folded w table (16 features) in bf16, the others the full one."""
     wl, (q, k, v), (qg, kg, vg), rowmap, fwd, geo = _setup(name, None, cuda)
     scale = scale_for(wl.dim)
     kv = K.kv_pack(kg, vg, rowmap, geo)
@@ -231,7 +234,7 @@ def test_coarse_tail(cuda, name):
     _, var = O.rotated_moments(kl, basis, counts, wl.video_tokens)
     basis, var = O.order_basis(basis, var, counts)
     cvk = O.value_key_covariance(kl, vl, km_ref, counts, wl.video_tokens)
-    w = O.fold_rank(var, 4)
+    w = O.fold_rank(var, rank)
     part = O.head_partition(ql, kl, scale, wl.density, wl.video_tokens)
     qv = ql[:, :wl.video_tokens].float()
     qsq = O.rotated_query_square(qv, basis, torch.bfloat16)
@@ -240,8 +243,10 @@ def test_coarse_tail(cuda, name):
                                    wl.video_tokens, torch.bfloat16)
     rows = geo.rows
     qt = K.basis_tables(basis.to(cuda), cvk.to(cuda), kv.dtype, query=True, cvk_table=True)
-    wt, kbar, vbar = K.coarse_tables(var.to(cuda), kv, 4)
-    tables = {"w": wt, "kbar": kbar, "vbar": vbar, "u_t": qt.u_t, "cvk_t": qt.cvk_t}
+    wt, kbar, vbar = K.coarse_tables(var.to(cuda), kv, rank)
+    assert wt.shape[-1] == (16 if 1 <= rank <= 13 and kv.dtype == torch.bfloat16 else wl.dim)
+    tables = {"w": wt, "kbar": kbar, "vbar": vbar, "u_t": qt.u_t, "cvk_t": qt.cvk_t,
+              "rank": rank}
     glref = torch.randn(kl.shape[0], rows, generator=torch.Generator().manual_seed(3)).to(cuda)
     go, gl, dpart = K.coarse_tail(qg, rowmap, part.to(cuda), geo, tables, scale, 2.0, glref)
     assert_close_bf16(go.cpu().float(), go_ref[:, :rows], f"coarse {name}")
