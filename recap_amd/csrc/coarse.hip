@@ -365,6 +365,7 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
   const float gs = pair_sum(gsum);
   const bool has_tail = l > 0.0f;
   const float safe_l = fmaxf(l, 1.0e-30f);
+  const float inv_l = 1.0f / safe_l;  // one division per row instead of one per element
   const float gfrac = T::to_f(T::from_f(has_tail ? gs / safe_l : 0.0f));
   const int64_t ri = (int64_t)bank * a.rows + r;
   uint16_t* gorow = a.go + ri * D;
@@ -379,7 +380,7 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
       float v[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float o = has_tail ? T::to_f(T::from_f(oacc[dt][4 * q4 + e] / safe_l)) : 0.0f;
+        const float o = has_tail ? T::to_f(T::from_f(oacc[dt][4 * q4 + e] * inv_l)) : 0.0f;
         const float dv = T::to_f(T::from_f(T::to_f(T::from_f(dacc[4 * q4 + e])) * a.scale));
         const float gd = T::to_f(T::from_f(gfrac * dv));
         v[e] = o + gd;
