@@ -201,6 +201,8 @@ int recap_block_scores(const float* q_means, const float* k_means, int64_t banks
                        int64_t n_blocks, int64_t dim, float scale, float* scores, void* stream) {
   REQUIRE(q_means && k_means && scores, "NULL pointer");
   REQUIRE(dim == 64 || dim == 128, "head dim %lld unsupported", (long long)dim);
+  REQUIRE(std::isfinite(scale) && scale > 0.0f, "scale must be positive and finite, got %g",
+          (double)scale);
   REQUIRE(banks >= 1 && n_blocks >= 1 && n_blocks <= 65535, "bad banks/n_blocks");
   ScoreArgs a{q_means, k_means, (int)banks, (int)n_blocks, (int)dim, scale, scores};
   return hip_status(run_block_scores(a, as_stream(stream)), "block_scores launch");
@@ -242,6 +244,8 @@ int recap_pool_select(const void* q, int dtype, int64_t batch, int64_t heads, in
   CHECK(check_tokens(n_tokens, n_video));
   REQUIRE(k_means && workspace && partition && kernel_mask, "NULL pointer");
   REQUIRE(density > 0.0 && density < 1.0, "density %g outside (0, 1)", density);
+  REQUIRE(std::isfinite(scale) && scale > 0.0f, "scale must be positive and finite, got %g",
+          (double)scale);
   REQUIRE(batch >= 1 && heads >= 1, "bad batch/heads");
   const Geom g = geometry(n_tokens, n_video);
   const int64_t banks = batch * heads;

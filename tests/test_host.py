@@ -76,6 +76,8 @@ def test_argument_validation_before_launch():
         with pytest.raises(ValueError, match="scale"):
             _lib.call("recap_block_sparse_attn", 16, _lib.RECAP_BF16, 1, 1, 64, 0, 0, 64, 16, 16,
                       16, 16, 256, bad, 16, 16, None)
+    with pytest.raises(ValueError, match="scale"):
+        _lib.call("recap_block_scores", 16, 16, 1, 4, 64, -0.125, 16, None)
     with pytest.raises(ValueError, match="theta"):
         _lib.call("recap_coarse_tail", 16, _lib.RECAP_BF16, 1, 1, 64, 0, 0, 64, 16, 16, 16, 16,
                   16, 16, 16, 256, 256, 0.125, -1.0, 4, None, 16, 16, 16, None)
