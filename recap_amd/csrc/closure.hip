@@ -15,11 +15,21 @@
 
 namespace recap {
 
+// Threads of a closure workgroup.  The per-call statistics at d = 128 (rotated moments and
+// C_vk) split the work by wave: waves 0-3 the rotation, waves 4-7 C_vk, so each wave holds
+// one job's registers and every SIMD runs two waves whose MFMA and VALU phases interleave.
+// Otherwise four waves each take one 32-row tile of every job.
+constexpr int closure_threads(int D, int FLAGS) {
+  return D == 128 && FLAGS == (kRot | kCvk) ? 512 : 256;
+}
+
 template <class T, int D, int FLAGS>
-__global__ __launch_bounds__(256, 1) void closure_kernel(ClosureArgs a) {
+__global__ __launch_bounds__(closure_threads(D, FLAGS), 1) void closure_kernel(ClosureArgs a) {
   using G = TileGeom<D>;
   constexpr int NS = D / 16, NT = D / 32;
   constexpr bool ROT = (FLAGS & kRot) != 0, CVK = (FLAGS & kCvk) != 0, SCAT = (FLAGS & kScatter) != 0;
+  constexpr int NTHR = closure_threads(D, FLAGS);
+  constexpr bool SPLIT = NTHR == 512;
   constexpr bool KC = SCAT;  // centred keys staged in LDS (the scatter's A and B operands)
   __shared__ __attribute__((aligned(16))) char k_lds[G::kTileBytes];
   __shared__ __attribute__((aligned(16))) char v_lds[CVK ? G::kTileBytes : 16];
@@ -30,10 +40,32 @@ __global__ __launch_bounds__(256, 1) void closure_kernel(ClosureArgs a) {
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, g = lane >> 5, l32 = lane & 31;
   const int bank = blockIdx.x / a.groups, grp = blockIdx.x % a.groups;
   const int j0 = grp * a.group, j1 = min(j0 + a.group, a.nb);
-  const int rot_tile = D == 128 ? wave : (wave < 2 ? wave : -1);
-  const int mat_tile = D == 128 ? wave : (wave >= 2 ? wave - 2 : -1);
+  const int rot_tile = SPLIT ? (wave < 4 ? wave : -1) : D == 128 ? wave : (wave < 2 ? wave : -1);
+  const int mat_tile = SPLIT ? (wave >= 4 ? wave - 4 : -1)
+                             : D == 128 ? wave : (wave >= 2 ? wave - 2 : -1);
 
-  u32x4 ub_hi[ROT ? NS : 1], ub_lo[ROT ? NS : 1];
+  // Registers that persist across blocks: a rotation wave's U^T hi/lo fragments (2 NS
+  // u32x4) and a C_vk wave's accumulators (NT f32x16).  In the split layout a wave has one
+  // job, never both, so the two share one array (64 registers at d = 128).
+  struct Quad { u32x4 v[4]; };
+  static_assert(!SPLIT || 2 * NS == 4 * NT, "shared persistent registers");
+  u32x4 ub[SPLIT ? 2 * NS : (ROT ? 2 * NS : 1)];
+  f32x16 cacc_own[!SPLIT && CVK ? NT : 1];
+  auto cget = [&](int mt) -> f32x16 {
+    if constexpr (SPLIT)
+      return __builtin_bit_cast(f32x16, Quad{{ub[4 * mt], ub[4 * mt + 1], ub[4 * mt + 2], ub[4 * mt + 3]}});
+    else
+      return cacc_own[mt];
+  };
+  auto cset = [&](int mt, f32x16 v) {
+    if constexpr (SPLIT) {
+      const Quad q = __builtin_bit_cast(Quad, v);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ub[4 * mt + i] = q.v[i];
+    } else {
+      cacc_own[mt] = v;
+    }
+  };
   if constexpr (ROT) {
     if (rot_tile >= 0) {
       const int o = 32 * rot_tile + l32;
@@ -41,8 +73,8 @@ __global__ __launch_bounds__(256, 1) void closure_kernel(ClosureArgs a) {
       const uint16_t* lo = a.u_lo_t + ((int64_t)bank * D + o) * D;
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
-        ub_hi[s] = *reinterpret_cast<const u32x4*>(hi + 16 * s + 8 * g);
-        ub_lo[s] = *reinterpret_cast<const u32x4*>(lo + 16 * s + 8 * g);
+        ub[s] = *reinterpret_cast<const u32x4*>(hi + 16 * s + 8 * g);
+        ub[NS + s] = *reinterpret_cast<const u32x4*>(lo + 16 * s + 8 * g);
       }
     }
   }
@@ -56,25 +88,29 @@ __global__ __launch_bounds__(256, 1) void closure_kernel(ClosureArgs a) {
     bid[hh] = u32x4{e >> 1 == 0 ? one : 0u, e >> 1 == 1 ? one : 0u, e >> 1 == 2 ? one : 0u,
                     e >> 1 == 3 ? one : 0u};
   }
-  f32x16 cacc[CVK ? NT : 1], sacc[SCAT ? NT : 1];
+  f32x16 sacc[SCAT ? NT : 1];
+  if constexpr (CVK) {
+    if (mat_tile >= 0) {
 #pragma unroll
-  for (int i = 0; i < (CVK ? NT : 1); ++i) cacc[i] = f32x16{};
+      for (int i = 0; i < NT; ++i) cset(i, f32x16{});
+    }
+  }
 #pragma unroll
   for (int i = 0; i < (SCAT ? NT : 1); ++i) sacc[i] = f32x16{};
 
   // The next block's K (and V^T) tile and mean are loaded into registers while this block
   // is processed, then stored into LDS at the top of the next iteration.
-  constexpr int KCH = G::kTileBytes / 16 / 256;  // 16-byte chunks per thread per tile
+  constexpr int KCH = G::kTileBytes / 16 / NTHR;  // 16-byte chunks per thread per tile
   u32x4 kpre[KCH], vpre[CVK ? KCH : 1];
   float mpre = 0.0f;
   auto load_block = [&](int j) {
     const u32x4* ks = reinterpret_cast<const u32x4*>(a.kp + ((int64_t)bank * a.tb + j) * G::kTileElems);
 #pragma unroll
-    for (int i = 0; i < KCH; ++i) kpre[i] = ks[t + 256 * i];
+    for (int i = 0; i < KCH; ++i) kpre[i] = ks[t + NTHR * i];
     if constexpr (CVK) {
       const u32x4* vs = reinterpret_cast<const u32x4*>(a.vp + ((int64_t)bank * a.tb + j) * G::kTileElems);
 #pragma unroll
-      for (int i = 0; i < KCH; ++i) vpre[i] = vs[t + 256 * i];
+      for (int i = 0; i < KCH; ++i) vpre[i] = vs[t + NTHR * i];
     }
     if (t < D) mpre = a.kmean[((int64_t)bank * a.nb + j) * D + t];
   };
@@ -82,10 +118,10 @@ __global__ __launch_bounds__(256, 1) void closure_kernel(ClosureArgs a) {
   for (int j = j0; j < j1; ++j) {
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < KCH; ++i) reinterpret_cast<u32x4*>(k_lds)[t + 256 * i] = kpre[i];
+    for (int i = 0; i < KCH; ++i) reinterpret_cast<u32x4*>(k_lds)[t + NTHR * i] = kpre[i];
     if constexpr (CVK) {
 #pragma unroll
-      for (int i = 0; i < KCH; ++i) reinterpret_cast<u32x4*>(v_lds)[t + 256 * i] = vpre[i];
+      for (int i = 0; i < KCH; ++i) reinterpret_cast<u32x4*>(v_lds)[t + NTHR * i] = vpre[i];
     }
     if (t < D) kmean_s[t] = mpre;
     if (j + 1 < j1) load_block(j + 1);
@@ -94,7 +130,7 @@ __global__ __launch_bounds__(256, 1) void closure_kernel(ClosureArgs a) {
 
     if constexpr (KC) {
       // Centred keys, transposed to [D][128 positions] (position p holds key swap23(p)).
-      for (int cc = t; cc < D * 16; cc += 256) {
+      for (int cc = t; cc < D * 16; cc += NTHR) {
         const int n = cc >> 4, c = cc & 15;
         unsigned whi[4], wlo[4];
 #pragma unroll
@@ -130,12 +166,12 @@ __global__ __launch_bounds__(256, 1) void closure_kernel(ClosureArgs a) {
 #pragma unroll
           for (int s = 0; s < NS; ++s) {
             const u32x4 ka = lds_load16(k_lds, G::k_off(32 * tt + l32, 2 * s + g));
-            racc[tt] = T::mfma32(ka, ub_hi[s], racc[tt]);
+            racc[tt] = T::mfma32(ka, ub[s], racc[tt]);
           }
 #pragma unroll
           for (int s = 0; s < NS; ++s) {
             const u32x4 ka = lds_load16(k_lds, G::k_off(32 * tt + l32, 2 * s + g));
-            racc[tt] = T::mfma32(ka, ub_lo[s], racc[tt]);
+            racc[tt] = T::mfma32(ka, ub[NS + s], racc[tt]);
           }
         }
         float s1 = 0.0f;
@@ -201,8 +237,9 @@ __global__ __launch_bounds__(256, 1) void closure_kernel(ClosureArgs a) {
 #pragma unroll
             for (int mt = 0; mt < NT; ++mt) {
               const u32x4 va = lds_load16(v_lds, G::vt_off(32 * mt + l32, 4 * tt + 2 * hh + g));
-              cacc[mt] = T::mfma32(va, bhi[hh], cacc[mt]);
-              cacc[mt] = T::mfma32(va, blo[hh], cacc[mt]);
+              f32x16 c = cget(mt);
+              c = T::mfma32(va, bhi[hh], c);
+              cset(mt, T::mfma32(va, blo[hh], c));
             }
         }
       }
@@ -237,7 +274,7 @@ __global__ __launch_bounds__(256, 1) void closure_kernel(ClosureArgs a) {
         // columns of tile nt.
         if constexpr (CVK)
           a.cvk_part[pbase + (int64_t)(32 * nt + mfma_row(rr, g)) * D + 32 * mat_tile + l32] =
-              cacc[nt][rr];
+              cget(nt)[rr];
         if constexpr (SCAT)
           a.scat_part[pbase + (int64_t)(32 * mat_tile + mfma_row(rr, g)) * D + 32 * nt + l32] =
               sacc[nt][rr];
@@ -247,11 +284,19 @@ __global__ __launch_bounds__(256, 1) void closure_kernel(ClosureArgs a) {
 
 template <class T, int D>
 static hipError_t launch_closure(const ClosureArgs& a, int flags, hipStream_t s) {
-  const dim3 grid((unsigned)(a.banks * a.groups)), block(256);
+  const dim3 grid((unsigned)(a.banks * a.groups));
   switch (flags) {
-    case kRot: hipLaunchKernelGGL((closure_kernel<T, D, kRot>), grid, block, 0, s, a); break;
-    case kCvk | kScatter: hipLaunchKernelGGL((closure_kernel<T, D, kCvk | kScatter>), grid, block, 0, s, a); break;
-    case kRot | kCvk: hipLaunchKernelGGL((closure_kernel<T, D, kRot | kCvk>), grid, block, 0, s, a); break;
+    case kRot:
+      hipLaunchKernelGGL((closure_kernel<T, D, kRot>), grid, dim3(closure_threads(D, kRot)), 0, s, a);
+      break;
+    case kCvk | kScatter:
+      hipLaunchKernelGGL((closure_kernel<T, D, kCvk | kScatter>), grid,
+                         dim3(closure_threads(D, kCvk | kScatter)), 0, s, a);
+      break;
+    case kRot | kCvk:
+      hipLaunchKernelGGL((closure_kernel<T, D, kRot | kCvk>), grid,
+                         dim3(closure_threads(D, kRot | kCvk)), 0, s, a);
+      break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
