@@ -27,6 +27,7 @@ Pinning status (how each function is checked, see tests/test_oracle.py):
   block_sparse_attention  textbook dense softmax with -inf outside the mask; LSE
   closure statistics    closed forms (covariance, eigh), rotation invariance, sign flips
   coarse_tail           brute-force per-row softmax; constant-block exactness case
+  gate_margin (helper)  brute-force scalar loop over (row, block) pairs
   sparse_merge/capture  refresh-then-sparse reproduces the dense output; alpha=0 case
 """
 
@@ -47,7 +48,7 @@ __all__ = [
     "within_block_scatter", "closure_basis", "split_hi_lo", "rotated_moments",
     "value_key_covariance", "order_basis", "fold_rank", "rotated_query_square",
     "value_drift", "coarse_tail", "drift_center", "sparse_merge", "refresh_detail",
-    "OracleLayer", "OracleOperator", "cast", "topk_margin",
+    "OracleLayer", "OracleOperator", "cast", "topk_margin", "gate_margin",
 ]
 
 
@@ -415,6 +416,31 @@ def coarse_tail(ql, qsq, drift, km, vm, w, counts, partition, scale, theta, n_vi
 
 
 # -- stage 4: drift weight, merge and refresh capture ---------------------------------------
+
+
+def gate_margin(qsq, w, partition, scale, theta, n_video, dtype, block=BLOCK):
+    """Test helper for the coarse tail's gate ``fl(s^2 qsq.w) <= theta^2``
+    (recap/kernels/coarse_tail.py:139-140): per reordered video row, the smallest relative
+    distance ``|fl(s^2 quad) - theta^2| / theta^2`` over the row's omitted blocks, with quad
+    computed as :func:`coarse_tail` does (fp64 dot of the type-rounded operands, rounded to
+    fp32).  Two fp32 summation orders of quad agree to ~1e-7 relative, so only rows with a
+    margin of that order can take a different gate decision.  Rows with no omitted block
+    get +inf.  Returns ``[banks, n_video]`` fp64."""
+    banks = qsq.shape[0]
+    nb = partition.shape[-1]
+    w16 = cast(w, dtype)
+    ssq, thsq = _f32(scale * scale), _f32(theta * theta)
+    out = torch.full((banks, n_video), math.inf, dtype=torch.float64)
+    for b in range(banks):
+        for i in range(nb):
+            r0, r1 = i * block, min((i + 1) * block, n_video)
+            omitted = torch.nonzero(~partition[b, i]).flatten()
+            if omitted.numel() == 0:
+                continue
+            quad = (qsq[b, r0:r1].double() @ w16[b, omitted].double().T).float()
+            rel = ((quad * ssq - thsq).abs() / thsq).double()
+            out[b, r0:r1] = rel.min(dim=-1).values
+    return out
 
 
 def drift_center(gl: torch.Tensor, glref: torch.Tensor) -> torch.Tensor:

@@ -46,13 +46,28 @@ def bf16_ulp(x: torch.Tensor) -> torch.Tensor:
     return torch.exp2(torch.floor(torch.log2(mag)) - 7)
 
 
+def bf16_tolerance(got: torch.Tensor, ref: torch.Tensor, max_abs: float = 2e-2) -> torch.Tensor:
+    """Per-element bound of a bf16 output against the oracle's fp32 output:
+    max(max_abs, 2 ulp_bf16(max(|got|, |ref|))).  The ulp term only matters for values >= 2,
+    where three roundings the two sides do not share add up: the output's own (0.5 ulp), the
+    reference's bf16 rounding of its head branch (recap/kernels/block_sparse.py stores a bf16
+    head, which the oracle follows; this build keeps it in fp32, 0.5 ulp), and the bf16
+    probabilities of the head's PV product (as in the reference's external attention kernel;
+    the oracle's head is exact): 2^-9 relative per term, up to ~1 ulp when one key dominates a
+    row of large values.  Measured worst case: 0.027 at 3.89 (Wan's value field, full
+    length).  The ulp is taken at the larger magnitude because the two can straddle a binade
+    boundary (reference 3.999 with a head rounded to 4.0, output 4.031 from a head of 4.016),
+    where the reference's own ulp is half the output's."""
+    mag = torch.maximum(got.abs(), ref.abs())
+    return torch.clamp_min(2.0 * bf16_ulp(mag), max_abs)
+
+
 def assert_close_bf16(got, ref, what, max_abs=2e-2, cos=0.999):
-    """bf16 output vs an fp32 reference: |err| <= max(max_abs, 1.5 ulp_bf16(ref)) and
-    cosine >= cos.  The ulp term only matters where |ref| >= 2, where one rounding of the
-    output plus one bf16 rounding inside the reference already reach 1.5 ulps."""
+    """bf16 output vs an fp32 reference: |err| <= bf16_tolerance(got, ref) and cosine >=
+    cos."""
     g, r = got.double().cpu(), ref.double().cpu()
     m, c = metrics(g, r)
-    tol = torch.clamp_min(1.5 * bf16_ulp(r), max_abs)
+    tol = bf16_tolerance(g, r, max_abs)
     excess = float(((g - r).abs() - tol).max())
     big = float((r.abs() >= 2).double().mean())
     print(f"[{what}] max_abs={m:.3e} cos={c:.6f} worst-vs-tolerance={excess:+.3e} "

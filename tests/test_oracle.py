@@ -464,6 +464,37 @@ def test_drift_center_is_the_mean_row_shift():
     torch.testing.assert_close(O.drift_center(gl, glref), torch.tensor([4.0 / 3.0, -1.0]))
 
 
+def test_gate_margin_brute_force():
+    # Scalar loop: for every (row, omitted block) pair the relative distance of the gate's
+    # fp32 product s^2 quad from theta^2, minimised per row; a planted pair sits exactly on
+    # the threshold (margin 0) and a fully kept query block gives +inf.
+    g = torch.Generator().manual_seed(21)
+    nv, d, nb, scale, theta = 300, 16, 3, 0.25, 2.0
+    qsq = (torch.rand(1, nv, d, generator=g) * 2).to(torch.bfloat16).float()
+    w = torch.rand(1, nb, d, generator=g) * 3
+    w[0, 1] = 0.0
+    w[0, 1, 0] = 1.0
+    qsq[0, 5, 0] = 64.0       # quad = 64 * 1.0 at block 1: s^2 quad = 4 = theta^2 exactly
+    part = torch.tensor([[[True, False, False], [False, True, False], [True, True, True]]])
+    got = O.gate_margin(qsq, w, part, scale, theta, nv, torch.bfloat16)
+    w16 = w.to(torch.bfloat16).double()
+    for r in range(nv):
+        i = r // 128
+        omitted = [j for j in range(nb) if not part[0, i, j]]
+        if not omitted:
+            assert got[0, r] == float("inf")
+            continue
+        best = math.inf
+        for j in omitted:
+            quad = float(torch.tensor(float((qsq[0, r].double() * w16[0, j]).sum()),
+                                      dtype=torch.float32))
+            prod = float(torch.tensor(quad, dtype=torch.float32) * torch.tensor(scale * scale,
+                                                                                  dtype=torch.float32))
+            best = min(best, abs(prod - theta * theta) / (theta * theta))
+        assert got[0, r] == pytest.approx(best, rel=1e-6, abs=1e-12), r
+    assert got[0, 5] == 0.0
+
+
 def test_topk_margin_brute_force():
     g = torch.Generator().manual_seed(14)
     s = torch.randn(3, 7, 20, generator=g)
