@@ -313,7 +313,10 @@ __global__ __launch_bounds__(256) void partial_reduce_kernel(const float* part, 
   if (idx >= (int64_t)banks * elems) return;
   const int64_t bank = idx / elems, e = idx % elems;
   const float* p = part + bank * groups * (int64_t)elems + e;
+  // Sequential order of the groups (fixed, so the result does not depend on the launch);
+  // unrolled so the loads of eight groups are in flight together.
   float acc = p[0];
+#pragma unroll 8
   for (int i = 1; i < groups; ++i) acc += p[(int64_t)i * elems];
   out[idx] = acc / divisor;
 }
