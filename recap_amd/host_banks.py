@@ -132,14 +132,13 @@ class HostBankOperator(Operator):
             K.bank_copy_async(dev, tensor, stream)
         return slot
 
-    def _split_in(self, bank, key_id) -> None:
+    def _split_in(self, bank, key_id, prefetched: bool) -> None:
+        """Point the bank at its split state in the split slot: already copied there with
+        the bank on the prefetch stream when `prefetched`, else copied now on the current
+        stream (recap/host_banks.py:116-130)."""
         if not self._host_split.get(key_id):
             return
-        if self._split_prefetched == key_id:
-            slot = self._split_slot(key_id)  # copied with the bank on the prefetch stream
-            self._split_prefetched = None
-        else:
-            slot = self._copy_split(key_id)
+        slot = self._split_slot(key_id) if prefetched else self._copy_split(key_id)
         for name in self._host_split[key_id]:
             setattr(bank, name, slot[name])
 
@@ -190,14 +189,24 @@ class HostBankOperator(Operator):
             torch.cuda.current_stream().wait_event(pending)
             self._slot_ready[index] = None
         self._device = query.device
+        # What the prefetch stream queued during the previous layer (normally this layer's
+        # bank and split state) is waited for here, before this layer touches a slot or
+        # queues the next layer's prefetch on that stream.  Which parts were for this layer
+        # is read now: _stage_in below starts the next prefetch and moves both markers on.
+        bank_ready = self._prefetched == key_id
+        split_ready = self._split_prefetched == key_id
+        if (self._prefetched is not None or self._split_prefetched is not None) \
+                and self._prefetch_stream is not None:
+            torch.cuda.current_stream().wait_stream(self._prefetch_stream)
+        self._prefetched = self._split_prefetched = None
         if self.kind == SPARSE:
             if host is None:
                 raise RuntimeError("a sparse call was requested before an exact refresh")
-            self._stage_in(key_id, slot)
+            self._stage_in(key_id, slot, bank_ready)
         elif bank.valid and host is not None:
-            self._stage_in(key_id, slot)  # the refresh scores the old refinement
+            self._stage_in(key_id, slot, bank_ready)  # the refresh scores the old refinement
         self._attach(bank, slot)
-        self._split_in(bank, key_id)
+        self._split_in(bank, key_id, split_ready)
         try:
             out = super().attend(layer_index, query, key, value)
         finally:
@@ -210,13 +219,12 @@ class HostBankOperator(Operator):
             self._detach(bank)
         return out
 
-    def _stage_in(self, key_id, slot: dict) -> None:
-        host = self._host[key_id]
-        if self._prefetched == key_id and self._prefetch_stream is not None:
-            torch.cuda.current_stream().wait_stream(self._prefetch_stream)
-            self._prefetched = None
-        else:
-            self._copy(slot, host, "h2d-sync")
+    def _stage_in(self, key_id, slot: dict, prefetched: bool) -> None:
+        """Bring the layer's bank into its slot: already there when `prefetched` (the
+        caller has waited for the prefetch stream), else a copy on the current stream.
+        Then start the next layer's prefetch."""
+        if not prefetched:
+            self._copy(slot, self._host[key_id], "h2d-sync")
         self._maybe_prefetch(key_id)
 
     def _maybe_prefetch(self, key_id) -> None:

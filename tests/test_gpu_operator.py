@@ -196,9 +196,19 @@ def test_host_banks_multi_step_schedule_identical(cuda, layers):
     inputs = [tuple(perturb(x, 0.03, seed=i, step=step) for i, x in enumerate(base))
               for step in range(len(schedule))]
     runs = {}
+    sync_split = []  # split-state copies queued on the compute stream by the prefetching run
     for label, kw in [("gpu", {}), ("host", {"host_banks": True}),
                       ("host-noprefetch", {"host_banks": True, "prefetch": False})]:
         op, _ = build(wl, layers=layers, **kw)
+        if label == "host":
+            copy_split = op._copy_split
+
+            def counted(key_id, stream=None, _inner=copy_split):
+                if stream is None:
+                    sync_split.append(key_id)
+                return _inner(key_id, stream)
+
+            op._copy_split = counted
         outs, stats = [], []
         for step, kind in enumerate(schedule):
             op.begin_step(step, kind)
@@ -215,6 +225,9 @@ def test_host_banks_multi_step_schedule_identical(cuda, layers):
             assert torch.equal(a, b), (label, i)
         assert runs["gpu"][1] == runs[label][1], label
     assert runs["gpu"][1][1] is not None  # the second refresh scored the first refinement
+    # With prefetch, a layer's split state arrives with its bank on the prefetch stream;
+    # only a layer nothing was prefetched for (layer 0 of a step, at most) copies it itself.
+    assert len(sync_split) <= len(schedule), sync_split
 
 
 @pytest.mark.parametrize("name", ["wan2.1-480p", "cogvideox1.5"])
