@@ -66,15 +66,31 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
     }
   }
 
-  // Stage a D x D matrix of the query type (rows of 8-element chunks) into LDS.
+  // Stage a D x D matrix of the query type (row-major in HBM) into LDS by buffer loads into
+  // LDS, all in flight at once: one wave instruction fills 1 KB of the swizzled image in lane
+  // order, so each lane fetches the logical chunk that its LDS position holds (the swizzle
+  // is an XOR, its own inverse).  The caller waits (vmcnt) and synchronises before reading.
   auto stage_matrix = [&](const uint16_t* src) {
-    for (int cc = t; cc < D * NCH / 2; cc += 256) {
-      const int row = cc / NCH, c = cc % NCH;
-      *reinterpret_cast<u32x4*>(st0 + G::k_off(row, c)) =
-          *reinterpret_cast<const u32x4*>(src + row * D + c * 8);
-      *reinterpret_cast<u32x4*>(st1 + G::k_off(row, c)) =
-          *reinterpret_cast<const u32x4*>(src + (row + D / 2) * D + c * 8);
+    constexpr int kHalfBytes = kMatBytes / 2;  // rows 0 .. D/2-1, and the rest
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)src, 0, kMatBytes, kBufferRsrcWord3);
+#pragma unroll
+    for (int i = 0; i < kHalfBytes / 4096; ++i) {
+      const int pos = 4096 * i + 16 * t;  // byte position in the half image
+      const int row = pos / (2 * D), pc = (pos % (2 * D)) >> 4;
+      const int from = row * 2 * D + ((pc ^ G::swz(row, NCH)) << 4);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(st0 + 4096 * i + 1024 * wave), 16,
+                                               from, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(st1 + 4096 * i + 1024 * wave), 16,
+                                               from + kHalfBytes, 0, 0, 0);
     }
+  };
+  // Wait for this wave's copies into LDS (and LDS accesses), then for every wave.
+  auto staged_barrier = [&]() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0x7 << 4);  // vmcnt(0) lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
   };
   // Fragment of row tile `rt` (32 rows) of a staged matrix; rt is a compile-time index.
   auto matrix_frag = [&](int rt, int chunk) {
@@ -91,7 +107,7 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
 #pragma unroll
     for (int s = 0; s < NS; ++s) qreg[s] = *reinterpret_cast<const u32x4*>(qrow + 16 * s + 8 * g);
   }
-  __syncthreads();
+  staged_barrier();
 
   // qsq = (U^T q)^2 in the query type (rotated value rounded, then its square rounded):
   // lane (g, l32) holds dims 32 ot + mfma_row(rr, g) of its row.  Full form: qsq in the
@@ -359,7 +375,7 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
   // Value drift s C_vk q in the output layout: stage C_vk over the tables' LDS.
   __syncthreads();
   stage_matrix(a.cvk + (int64_t)bank * D * D);
-  __syncthreads();
+  staged_barrier();
 
   const float l = pair_sum(lsum);
   const float gs = pair_sum(gsum);
