@@ -414,7 +414,10 @@ static int attn_common(const void* q, int dtype, int64_t batch, int64_t heads, i
   a.kp = static_cast<const uint16_t*>(k_tiles); a.vp = static_cast<const uint16_t*>(vt_tiles);
   a.rowmap = rowmap;
   a.heads = (int)heads; a.banks = (int)(batch * heads);
-  a.n_tokens = (int)n_tokens; a.tb = (int)g.tb; a.ds = (int)g.ds;
+  a.n_tokens = (int)n_tokens; a.tb = (int)g.tb;
+  // Long rows, started first: the text rows (from ds) and a ragged last video block, which
+  // the selection keeps dense (recap/sparse/attention.py:88-94).
+  a.ds = (int)((n_video % kBlock) != 0 ? g.nb - 1 : g.ds);
   a.rows = (int)g.rows;
   return RECAP_OK;
 }

@@ -172,15 +172,25 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
 
   const int t = threadIdx.x, lane = t & 63, g = lane >> 5, l32 = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-  // Runs of 64 query blocks per XCD (about the workgroups one XCD holds at once): the
-  // neighbouring Hilbert-ordered blocks in flight on an XCD share many key tiles in its L2,
-  // and all XCDs together stay within ~512 blocks of one bank, whose K/V images (58 MB at
-  // the HunyuanVideo shape) stay in the 256 MB Infinity Cache.
-  const int lin = xcd_runs(blockIdx.x, gridDim.x, 64);
-  const int bank = lin / a.tb;
-  const int k_in_bank = lin % a.tb;
-  const int ndense = a.tb - a.ds;  // dense query blocks first: they are the longest
-  const int qt = k_in_bank < ndense ? a.ds + k_in_bank : k_in_bank - ndense;
+  // Work items.  The long rows of every bank (query blocks ds .. tb-1: the text rows and a
+  // ragged last video block, all dense) come first, dealt round-robin over the XCDs
+  // (workgroup i runs on XCD i % 8): they start before the short ones and every XCD gets an
+  // equal share.  The other rows follow in runs of 64 query blocks per XCD (about the
+  // workgroups one XCD holds at once): the neighbouring Hilbert-ordered blocks in flight on
+  // an XCD share many key tiles in its L2, and all XCDs together stay within ~512 blocks of
+  // one bank, whose K/V images (58 MB at the HunyuanVideo shape) stay in the 256 MB
+  // Infinity Cache.
+  const int nlong = a.tb - a.ds, nshort = a.ds;
+  const int n_long_items = a.banks * nlong;
+  int bank, qt;
+  if ((int)blockIdx.x < n_long_items) {
+    bank = blockIdx.x / nlong;
+    qt = a.ds + blockIdx.x % nlong;
+  } else {
+    const int lin = xcd_runs(blockIdx.x - n_long_items, gridDim.x - n_long_items, 64);
+    bank = lin / nshort;
+    qt = lin % nshort;
+  }
   const int b = bank / a.heads, h = bank % a.heads;
 
   int nkeep = a.tb;

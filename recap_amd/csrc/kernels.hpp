@@ -97,7 +97,8 @@ struct AttnArgs {
   const uint16_t* q; int64_t qsB, qsH, qsN;
   const uint16_t* kp; const uint16_t* vp;
   const int32_t* rowmap; const uint8_t* kmask;   // kmask null in dense mode
-  int heads, banks, n_tokens, tb, ds;
+  int heads, banks, n_tokens, tb;
+  int ds;                                        // first long (dense) query row, started first
   float scale_log2;
   float* head_out; float* head_lse;              // head / dense-head, reordered [bank][N](D), fp32
   uint16_t* out; int64_t osB, osH, osN;          // dense / dense-head / merge, native order
