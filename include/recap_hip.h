@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define RECAP_ABI_VERSION 2
+#define RECAP_ABI_VERSION 3
 
 enum { RECAP_OK = 0, RECAP_EINVAL = 1, RECAP_EUNSUPPORTED = 2, RECAP_EHIP = 3 };
 enum { RECAP_F16 = 1, RECAP_BF16 = 2 };
@@ -203,7 +203,8 @@ int recap_dense_head_attn(const void* q, int dtype, int64_t batch, int64_t heads
                           const void* k_tiles, const void* vt_tiles, const int32_t* rowmap,
                           const uint8_t* kernel_mask, int64_t n_tokens, float scale, void* out,
                           int64_t out_stride_b, int64_t out_stride_h, int64_t out_stride_n,
-                          float* lse, float* head_out, float* head_lse, void* stream);
+                          float* lse, float* head_out, float* head_lse, uint32_t* work_queue,
+                          void* stream);
 
 /* Dense attention with LSE, native order: out [batch, heads, n_tokens, dim] with the
  * given strides, lse [banks, n_tokens].
@@ -228,7 +229,16 @@ int recap_sparse_merge_attn(const void* q, int dtype, int64_t batch, int64_t hea
                             float scale, const void* go, const float* gl, const void* det,
                             const float* dl, const float* glref, const float* center,
                             float alpha_override, void* out, int64_t out_stride_b,
-                            int64_t out_stride_h, int64_t out_stride_n, void* stream);
+                            int64_t out_stride_h, int64_t out_stride_n, uint32_t* work_queue,
+                            void* stream);
+
+/* Words of the optional `work_queue` of recap_dense_head_attn and recap_sparse_merge_attn
+ * (16-byte aligned device memory, contents ignored: the call zeroes it on `stream` before the
+ * launch).  With it, workgroups claim their query blocks from per-XCD queues and XCDs that
+ * finish early take the others' last blocks; NULL keeps the static assignment.  Outputs are
+ * identical either way.  Calls that may overlap need separate queues.  No counterpart in
+ * the reference (the external kernel schedules itself). */
+int64_t recap_attn_queue_words(void);
 
 /* Stage 4 ------------------------------------------------------------------------------ */
 

@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "librecap_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 RECAP_OK, RECAP_EINVAL, RECAP_EUNSUPPORTED, RECAP_EHIP = 0, 1, 2, 3
 RECAP_F16, RECAP_BF16 = 1, 2
@@ -51,9 +51,10 @@ SIGNATURES: dict[str, tuple] = {
     "recap_dense_attn": (_I, [_P, _I, _I64, _I64, _I64, *_STRIDES, _P, _P, _P, _I64, _F, _P,
                               *_STRIDES, _P, _P]),
     "recap_dense_head_attn": (_I, [_P, _I, _I64, _I64, _I64, *_STRIDES, _P, _P, _P, _P, _I64, _F,
-                                   _P, *_STRIDES, _P, _P, _P, _P]),
+                                   _P, *_STRIDES, _P, _P, _P, _P, _P]),
     "recap_sparse_merge_attn": (_I, [_P, _I, _I64, _I64, _I64, *_STRIDES, _P, _P, _P, _P, _I64,
-                                     _I64, _F, _P, _P, _P, _P, _P, _P, _F, _P, *_STRIDES, _P]),
+                                     _I64, _F, _P, _P, _P, _P, _P, _P, _F, _P, *_STRIDES, _P, _P]),
+    "recap_attn_queue_words": (_I64, []),
     "recap_capture_partials": (_I64, [_I64, _I64, _I64]),
     "recap_refresh_capture": (_I, [_P, _I, _I64, _I64, _I64, *_STRIDES, _P, _P, _P, _P, _P, _P,
                                    _I64, _I64, _P, _P, _P, _P, _P, _P, _P]),

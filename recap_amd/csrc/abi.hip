@@ -93,6 +93,17 @@ int set_scale(AttnArgs& a, float scale) {
     if (_rc != RECAP_OK) return _rc; \
   } while (0)
 
+// Optional claim queues of an attention launch: zeroed on the stream (a fill kernel, so a
+// captured graph records no memset) right before the launch that uses them.
+int set_queue(AttnArgs& a, uint32_t* queue, hipStream_t s) {
+  a.queue = nullptr;
+  if (queue == nullptr) return RECAP_OK;
+  REQUIRE(aligned16(queue), "work_queue must be 16-byte aligned");
+  CHECK(hip_status(run_zero_words(queue, kQueueWords, s), "work_queue reset"));
+  a.queue = queue;
+  return RECAP_OK;
+}
+
 hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 }  // namespace
@@ -461,7 +472,8 @@ int recap_dense_head_attn(const void* q, int dtype, int64_t batch, int64_t heads
                           const void* k_tiles, const void* vt_tiles, const int32_t* rowmap,
                           const uint8_t* kernel_mask, int64_t n_tokens, float scale, void* out,
                           int64_t out_stride_b, int64_t out_stride_h, int64_t out_stride_n,
-                          float* lse, float* head_out, float* head_lse, void* stream) {
+                          float* lse, float* head_out, float* head_lse, uint32_t* work_queue,
+                          void* stream) {
   AttnArgs a{};
   CHECK(attn_common(q, dtype, batch, heads, dim, stride_b, stride_h, stride_n, k_tiles, vt_tiles,
                     rowmap, n_tokens, n_tokens, a));
@@ -474,6 +486,7 @@ int recap_dense_head_attn(const void* q, int dtype, int64_t batch, int64_t heads
   a.out = static_cast<uint16_t*>(out); a.osB = out_stride_b; a.osH = out_stride_h; a.osN = out_stride_n;
   a.lse_native = lse;
   a.head_out = head_out; a.head_lse = head_lse;
+  CHECK(set_queue(a, work_queue, as_stream(stream)));
   return hip_status(run_attention(a, dtype, (int)dim, kModeDenseHead, as_stream(stream)), "attention launch");
 }
 
@@ -484,7 +497,8 @@ int recap_sparse_merge_attn(const void* q, int dtype, int64_t batch, int64_t hea
                             float scale, const void* go, const float* gl, const void* det,
                             const float* dl, const float* glref, const float* center,
                             float alpha_override, void* out, int64_t out_stride_b,
-                            int64_t out_stride_h, int64_t out_stride_n, void* stream) {
+                            int64_t out_stride_h, int64_t out_stride_n, uint32_t* work_queue,
+                            void* stream) {
   AttnArgs a{};
   CHECK(attn_common(q, dtype, batch, heads, dim, stride_b, stride_h, stride_n, k_tiles, vt_tiles,
                     rowmap, n_tokens, n_video, a));
@@ -501,8 +515,11 @@ int recap_sparse_merge_attn(const void* q, int dtype, int64_t batch, int64_t hea
   a.dl = dl; a.glref = glref; a.center = center;
   a.use_override = alpha_override >= 0.0f ? 1 : 0;
   a.alpha_override = alpha_override;
+  CHECK(set_queue(a, work_queue, as_stream(stream)));
   return hip_status(run_attention(a, dtype, (int)dim, kModeMerge, as_stream(stream)), "attention launch");
 }
+
+int64_t recap_attn_queue_words(void) { return kQueueWords; }
 
 int64_t recap_capture_partials(int64_t banks, int64_t dim, int64_t n_video) {
   if (banks < 1 || (dim != 64 && dim != 128) || n_video < 1) return -1;

@@ -180,14 +180,44 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
   // an XCD share many key tiles in its L2, and all XCDs together stay within ~512 blocks of
   // one bank, whose K/V images (58 MB at the HunyuanVideo shape) stay in the 256 MB
   // Infinity Cache.
+  //
+  // With a queue the workgroups are persistent (about two per CU) and claim their items:
+  // XCD x holds the positions p = x, x + 8, x + 16, ... in that order, and a workgroup takes
+  // the next one of its own XCD (one atomic increment) or, once those are all taken, of the
+  // next XCD that still has one; it stops when every queue is empty.  XCDs that run faster
+  // then process the slower ones' last items instead of idling.  Every increment below an
+  // XCD's count claims a distinct position, so each item is processed exactly once.
+  __shared__ int claimed;
+  const int n_items = a.banks * a.tb;
+  const bool persistent = a.queue != nullptr;
+  for (int round = 0;; ++round) {
+  int pos = blockIdx.x;
+  if (persistent) {
+    if (t == 0) {
+      const int own = blockIdx.x & 7;
+      int got = -1;
+      for (int k = 0; k < 8 && got < 0; ++k) {
+        const int x = (own + k) & 7;
+        const int count = (n_items - x + 7) >> 3;  // positions on XCD x
+        const int i = (int)atomicAdd(a.queue + kQueueStride * x, 1u);
+        if (i < count) got = 8 * i + x;
+      }
+      claimed = got;  // -1: every queue is empty
+    }
+    __syncthreads();
+    pos = __builtin_amdgcn_readfirstlane(claimed);
+    if (pos < 0) break;
+  } else if (round > 0) {
+    break;
+  }
   const int nlong = a.tb - a.ds, nshort = a.ds;
   const int n_long_items = a.banks * nlong;
   int bank, qt;
-  if ((int)blockIdx.x < n_long_items) {
-    bank = blockIdx.x / nlong;
-    qt = a.ds + blockIdx.x % nlong;
+  if (pos < n_long_items) {
+    bank = pos / nlong;
+    qt = a.ds + pos % nlong;
   } else {
-    const int lin = xcd_runs(blockIdx.x - n_long_items, gridDim.x - n_long_items, 64);
+    const int lin = xcd_runs(pos - n_long_items, n_items - n_long_items, 64);
     bank = lin / nshort;
     qt = lin % nshort;
   }
@@ -496,17 +526,40 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
     const float lt = pair_sum(lsum[q]);  // lanes l and l ^ 32 share one row: both valid or not
     if (valid[q]) store_rows<T, D, kStore>(a, bank, b, h, row[q], nat[q], g, oacc[q], m[q], lt);
   }
+  __syncthreads();  // every wave is done with the LDS slots, the list and `claimed`
+  }  // items
+}
+
+// Workgroups of a persistent launch: two per CU (the attention kernel's occupancy), no
+// more than there are items.
+static int persistent_grid(int items) {
+  int device = 0, cus = 0;
+  if (hipGetDevice(&device) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+      cus < 1)
+    cus = 256;
+  return items < 2 * cus ? items : 2 * cus;
 }
 
 template <class T, int D>
 static hipError_t launch_attention(const AttnArgs& a, int mode, hipStream_t s) {
-  const dim3 grid((unsigned)(a.banks * a.tb)), block(kThreads);
+  const int items = a.banks * a.tb;
+  const dim3 grid((unsigned)(a.queue != nullptr ? persistent_grid(items) : items)), block(kThreads);
   switch (mode) {
     case kModeHead: hipLaunchKernelGGL((attention_kernel<T, D, kModeHead>), grid, block, 0, s, a); break;
     case kModeDense: hipLaunchKernelGGL((attention_kernel<T, D, kModeDense>), grid, block, 0, s, a); break;
     case kModeDenseHead: hipLaunchKernelGGL((attention_kernel<T, D, kModeDenseHead>), grid, block, 0, s, a); break;
     default: hipLaunchKernelGGL((attention_kernel<T, D, kModeMerge>), grid, block, 0, s, a); break;
   }
+  return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void zero_words_kernel(unsigned* p, int n) {
+  for (int i = threadIdx.x; i < n; i += 256) p[i] = 0u;
+}
+
+hipError_t run_zero_words(unsigned* p, int n, hipStream_t s) {
+  hipLaunchKernelGGL(zero_words_kernel, dim3(1), dim3(256), 0, s, p, n);
   return hipGetLastError();
 }
 

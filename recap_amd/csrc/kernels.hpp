@@ -105,8 +105,13 @@ struct AttnArgs {
   float* lse_native;                             // dense / dense-head [bank][N]
   int rows; const uint16_t* go; const float* gl; const uint16_t* det; const float* dl;
   const float* glref; const float* center; float alpha_override; int use_override;
+  unsigned* queue;   // kQueueWords zeroed words: per-XCD claim counters, or null (static)
 };
 hipError_t run_attention(const AttnArgs& a, int dtype, int dim, int mode, hipStream_t s);
+// Claim counters of the attention launch's work queues: one per XCD, 128 bytes apart.
+constexpr int kQueueStride = 32;
+constexpr int kQueueWords = 8 * kQueueStride;
+hipError_t run_zero_words(unsigned* p, int n, hipStream_t s);
 
 // Refresh capture (capture.hip).
 struct CaptureArgs {

@@ -359,11 +359,21 @@ def dense_attn(q: torch.Tensor, kv: PackedKV, rowmap: torch.Tensor, scale: float
     return out, lse
 
 
+def _work_queue(device, balance: bool):
+    """Claim counters for a load-balanced attention launch (zeroed by the call), or None."""
+    if not balance:
+        return None
+    return torch.empty(int(_lib.load().recap_attn_queue_words()), dtype=torch.int32,
+                       device=device)
+
+
 def dense_head_attn(q: torch.Tensor, kv: PackedKV, rowmap: torch.Tensor,
-                    kernel_mask: torch.Tensor, scale: float, out: torch.Tensor | None = None):
+                    kernel_mask: torch.Tensor, scale: float, out: torch.Tensor | None = None,
+                    balance: bool = True):
     """A refresh's dense attention and head branch in one pass:
     (out [B, H, N, d] native, lse [B, H, N], head_out [banks, N, d] fp32 reordered,
-    head_lse [banks, N])."""
+    head_lse [banks, N]).  `balance` lets XCDs that finish early take the others' last query
+    blocks (same outputs)."""
     b, h, n, d = q.shape
     kernel_mask = kernel_mask.contiguous()
     if out is None:
@@ -374,15 +384,16 @@ def dense_head_attn(q: torch.Tensor, kv: PackedKV, rowmap: torch.Tensor,
     call("recap_dense_head_attn", *_qkv_args(q), kv.k_tiles.data_ptr(), kv.vt_tiles.data_ptr(),
          rowmap.data_ptr(), kernel_mask.data_ptr(), n, float(scale), out.data_ptr(),
          out.stride(0), out.stride(1), out.stride(2), lse.data_ptr(), head_out.data_ptr(),
-         head_lse.data_ptr(), _stream())
+         head_lse.data_ptr(), _p(_work_queue(q.device, balance)), _stream())
     return out, lse, head_out, head_lse
 
 
 def sparse_merge_attn(q: torch.Tensor, kv: PackedKV, rowmap: torch.Tensor,
                       kernel_mask: torch.Tensor, geo: Geometry, scale: float, go, gl, det, dl,
                       glref, center, alpha_override: float | None = None,
-                      out: torch.Tensor | None = None) -> torch.Tensor:
-    """Corrected sparse output [B, H, N, d] in native order (one fused kernel)."""
+                      out: torch.Tensor | None = None, balance: bool = True) -> torch.Tensor:
+    """Corrected sparse output [B, H, N, d] in native order (one fused kernel); `balance` as
+    for dense_head_attn."""
     b, h, n, d = q.shape
     kernel_mask = kernel_mask.contiguous()
     if any(t is not None and not t.is_contiguous() for t in (go, gl, det, dl, glref, center)):
@@ -393,7 +404,8 @@ def sparse_merge_attn(q: torch.Tensor, kv: PackedKV, rowmap: torch.Tensor,
     call("recap_sparse_merge_attn", *_qkv_args(q), kv.k_tiles.data_ptr(),
          kv.vt_tiles.data_ptr(), rowmap.data_ptr(), kernel_mask.data_ptr(), n, geo.n_video,
          float(scale), _p(go), _p(gl), _p(det), _p(dl), _p(glref), _p(center), alpha,
-         out.data_ptr(), out.stride(0), out.stride(1), out.stride(2), _stream())
+         out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
+         _p(_work_queue(q.device, balance)), _stream())
     return out
 
 

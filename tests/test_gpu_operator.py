@@ -324,3 +324,31 @@ def test_hunyuan_bank_chunks_and_host_banks_are_identical(hunyuan_inputs):
     for label in ("chunks4", "host", "host-noprefetch"):
         for a, b in zip(outs["plain"], outs[label]):
             assert torch.equal(a, b), label
+
+
+@pytest.mark.parametrize("name", ["wan2.1-480p", "hunyuan-720p"])
+def test_work_queue_schedule_gives_identical_outputs(cuda, monkeypatch, name):
+    """The attention launches with per-XCD claim queues (XCDs that finish early take the
+    others' last query blocks) and with the static assignment give bit-identical refresh
+    and sparse outputs: only which workgroup computes a query block changes."""
+    from recap_amd import kernels as K
+    wl = WORKLOADS[name]
+    print(f"case {name}", flush=True)
+    q, k, v = make_qkv(wl, seed=0, device=cuda)
+    q1, k1, v1 = (perturb(x, 0.02, seed=i, step=1) for i, x in enumerate((q, k, v)))
+    outs = {}
+    dense_head, merge = K.dense_head_attn, K.sparse_merge_attn
+    for balance in (True, False):
+        monkeypatch.setattr(K, "dense_head_attn",
+                            lambda *a, **kw: dense_head(*a, **kw, balance=balance))
+        monkeypatch.setattr(K, "sparse_merge_attn",
+                            lambda *a, **kw: merge(*a, **kw, balance=balance))
+        op, _ = build(wl, layers=1)
+        op.begin_step(0, REFRESH)
+        dense = op.attend(0, q, k, v).clone()
+        op.begin_step(1, SPARSE)
+        sparse = op.attend(0, q1, k1, v1).clone()
+        outs[balance] = (dense, sparse)
+        print(f"  balance={balance}: done", flush=True)
+    assert torch.equal(outs[True][0], outs[False][0])
+    assert torch.equal(outs[True][1], outs[False][1])

@@ -65,7 +65,11 @@ def test_argument_validation_before_launch():
                   _lib.CLOSURE_SCATTER, 16, 16, 16, None)
     with pytest.raises(ValueError, match="drift weight"):
         _lib.call("recap_sparse_merge_attn", 16, _lib.RECAP_BF16, 1, 1, 64, 0, 0, 64, 16, 16, 16,
-                  16, 256, 256, 0.125, 16, 16, 16, 16, None, None, -1.0, 16, 0, 0, 64, None)
+                  16, 256, 256, 0.125, 16, 16, 16, 16, None, None, -1.0, 16, 0, 0, 64, None, None)
+    with pytest.raises(ValueError, match="work_queue"):
+        _lib.call("recap_sparse_merge_attn", 16, _lib.RECAP_BF16, 1, 1, 64, 0, 0, 64, 16, 16, 16,
+                  16, 256, 256, 0.125, 16, 16, 16, 16, None, None, 0.5, 16, 0, 0, 64, 20, None)
+    assert _lib.load().recap_attn_queue_words() == 256
     with pytest.raises(ValueError, match="kernel blocks"):
         _lib.call("recap_dense_attn", 16, _lib.RECAP_BF16, 1, 1, 64, 0, 0, 64, 16, 16, 16,
                   2049 * 128, 0.125, 16, 0, 0, 64, 16, None)
