@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define RECAP_ABI_VERSION 3
+#define RECAP_ABI_VERSION 4
 
 enum { RECAP_OK = 0, RECAP_EINVAL = 1, RECAP_EUNSUPPORTED = 2, RECAP_EHIP = 3 };
 enum { RECAP_F16 = 1, RECAP_BF16 = 2 };
@@ -182,19 +182,21 @@ int recap_drift_center(const float* drift_partial, int64_t banks, int64_t n_vide
 /* Stage 2 ------------------------------------------------------------------------------ */
 
 /* Head branch at a refresh: exact attention over the kernel mask, reordered order:
- * head_out [banks, n_tokens, dim] fp32, head_lse [banks, n_tokens] (natural log).
+ * head_out [banks, n_tokens, dim] in `dtype` (the external kernel returns its output in
+ * the input type), head_lse [banks, n_tokens] fp32 (natural log).
  * Replaces block_sparse_exact, recap/kernels/block_sparse.py:78-139. */
 int recap_block_sparse_attn(const void* q, int dtype, int64_t batch, int64_t heads,
                             int64_t dim, int64_t stride_b, int64_t stride_h, int64_t stride_n,
                             const void* k_tiles, const void* vt_tiles, const int32_t* rowmap,
                             const uint8_t* kernel_mask, int64_t n_tokens, float scale,
-                            float* head_out, float* head_lse, void* stream);
+                            void* head_out, float* head_lse, void* stream);
 
 /* A refresh's two attention results in one pass over the keys: the dense output and LSE
  * as recap_dense_attn, and the head branch of `kernel_mask` as recap_block_sparse_attn
- * (head_out [banks, n_tokens, dim] fp32 and head_lse [banks, n_tokens], reordered rows).
- * Each query block walks its kept key blocks first and stores the head branch from the
- * running softmax state when they are done, then walks the rest.
+ * (head_out [banks, n_tokens, dim] in `dtype` and head_lse [banks, n_tokens], reordered
+ * rows; bit-identical to recap_block_sparse_attn's).  Each query block walks its kept key
+ * blocks first and stores the head branch from the running softmax state when they are
+ * done, then walks the rest.
  * Replaces the two attention calls of a refresh: aten._scaled_dot_product_flash_attention,
  * recap/operator.py:254-256, and block_sparse_exact, recap/operator.py:345-346 with
  * recap/kernels/block_sparse.py:78-139. */
@@ -203,7 +205,7 @@ int recap_dense_head_attn(const void* q, int dtype, int64_t batch, int64_t heads
                           const void* k_tiles, const void* vt_tiles, const int32_t* rowmap,
                           const uint8_t* kernel_mask, int64_t n_tokens, float scale, void* out,
                           int64_t out_stride_b, int64_t out_stride_h, int64_t out_stride_n,
-                          float* lse, float* head_out, float* head_lse, uint32_t* work_queue,
+                          float* lse, void* head_out, float* head_lse, uint32_t* work_queue,
                           void* stream);
 
 /* Dense attention with LSE, native order: out [batch, heads, n_tokens, dim] with the
@@ -246,14 +248,15 @@ int64_t recap_attn_queue_words(void);
 int64_t recap_capture_partials(int64_t banks, int64_t dim, int64_t n_video);
 
 /* Refinement capture in place into det (fp16 [banks, R, dim]) and dl ([banks, R]) from the
- * dense output (native order, query type), the fp32 head branch and the coarse tail.  With
+ * dense output (native order, query type), the head branch (query type, as written by
+ * recap_block_sparse_attn or recap_dense_head_attn) and the coarse tail.  With
  * glref and center non-NULL the previous refinement is scored first: stat_partial
  * receives the partial pairs and stats[2] = (sum err^2, sum ref^2).
  * Replaces refresh_detail + _refresh_detail_kernel, recap/kernels/detail_cache.py:25-186,
  * 304-379. */
 int recap_refresh_capture(const void* dense_out, int dtype, int64_t batch, int64_t heads,
                           int64_t dim, int64_t out_stride_b, int64_t out_stride_h,
-                          int64_t out_stride_n, const float* dense_lse, const float* head_out,
+                          int64_t out_stride_n, const float* dense_lse, const void* head_out,
                           const float* head_lse, const void* go, const float* gl,
                           const int32_t* rowmap, int64_t n_tokens, int64_t n_video, void* det,
                           float* dl, const float* glref, const float* center,

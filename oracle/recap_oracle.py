@@ -29,6 +29,10 @@ Pinning status (how each function is checked, see tests/test_oracle.py):
   coarse_tail           brute-force per-row softmax; constant-block exactness case
   gate_margin (helper)  brute-force scalar loop over (row, block) pairs
   sparse_merge/capture  refresh-then-sparse reproduces the dense output; alpha=0 case
+  refresh_detail stats  closed forms of the old sparse output for an offset refinement, an
+                        offset log-mass and a per-row drift weight below one
+  OracleOperator rerank the new partition is the fresh head_partition; the recaptured
+                        refinement reproduces the dense output on the refresh inputs
 """
 
 from __future__ import annotations

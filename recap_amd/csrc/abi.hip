@@ -437,7 +437,7 @@ int recap_block_sparse_attn(const void* q, int dtype, int64_t batch, int64_t hea
                             int64_t dim, int64_t stride_b, int64_t stride_h, int64_t stride_n,
                             const void* k_tiles, const void* vt_tiles, const int32_t* rowmap,
                             const uint8_t* kernel_mask, int64_t n_tokens, float scale,
-                            float* head_out, float* head_lse, void* stream) {
+                            void* head_out, float* head_lse, void* stream) {
   AttnArgs a{};
   // The head branch does not use the video/text split; any n_video <= n_tokens works.
   CHECK(attn_common(q, dtype, batch, heads, dim, stride_b, stride_h, stride_n, k_tiles, vt_tiles,
@@ -446,7 +446,7 @@ int recap_block_sparse_attn(const void* q, int dtype, int64_t batch, int64_t hea
   REQUIRE(aligned16(head_out), "head_out must be 16-byte aligned");
   a.kmask = kernel_mask; a.ds = a.tb;
   CHECK(set_scale(a, scale));
-  a.head_out = head_out; a.head_lse = head_lse;
+  a.head_out = static_cast<uint16_t*>(head_out); a.head_lse = head_lse;
   return hip_status(run_attention(a, dtype, (int)dim, kModeHead, as_stream(stream)), "attention launch");
 }
 
@@ -472,7 +472,7 @@ int recap_dense_head_attn(const void* q, int dtype, int64_t batch, int64_t heads
                           const void* k_tiles, const void* vt_tiles, const int32_t* rowmap,
                           const uint8_t* kernel_mask, int64_t n_tokens, float scale, void* out,
                           int64_t out_stride_b, int64_t out_stride_h, int64_t out_stride_n,
-                          float* lse, float* head_out, float* head_lse, uint32_t* work_queue,
+                          float* lse, void* head_out, float* head_lse, uint32_t* work_queue,
                           void* stream) {
   AttnArgs a{};
   CHECK(attn_common(q, dtype, batch, heads, dim, stride_b, stride_h, stride_n, k_tiles, vt_tiles,
@@ -485,7 +485,7 @@ int recap_dense_head_attn(const void* q, int dtype, int64_t batch, int64_t heads
   CHECK(set_scale(a, scale));
   a.out = static_cast<uint16_t*>(out); a.osB = out_stride_b; a.osH = out_stride_h; a.osN = out_stride_n;
   a.lse_native = lse;
-  a.head_out = head_out; a.head_lse = head_lse;
+  a.head_out = static_cast<uint16_t*>(head_out); a.head_lse = head_lse;
   CHECK(set_queue(a, work_queue, as_stream(stream)));
   return hip_status(run_attention(a, dtype, (int)dim, kModeDenseHead, as_stream(stream)), "attention launch");
 }
@@ -529,7 +529,7 @@ int64_t recap_capture_partials(int64_t banks, int64_t dim, int64_t n_video) {
 
 int recap_refresh_capture(const void* dense_out, int dtype, int64_t batch, int64_t heads,
                           int64_t dim, int64_t out_stride_b, int64_t out_stride_h,
-                          int64_t out_stride_n, const float* dense_lse, const float* head_out,
+                          int64_t out_stride_n, const float* dense_lse, const void* head_out,
                           const float* head_lse, const void* go, const float* gl,
                           const int32_t* rowmap, int64_t n_tokens, int64_t n_video, void* det,
                           float* dl, const float* glref, const float* center,
@@ -546,7 +546,7 @@ int recap_refresh_capture(const void* dense_out, int dtype, int64_t batch, int64
   CaptureArgs a{};
   a.of = static_cast<const uint16_t*>(dense_out);
   a.osB = out_stride_b; a.osH = out_stride_h; a.osN = out_stride_n;
-  a.lf = dense_lse; a.oh = head_out; a.lh = head_lse;
+  a.lf = dense_lse; a.oh = static_cast<const uint16_t*>(head_out); a.lh = head_lse;
   a.go = static_cast<const uint16_t*>(go); a.gl = gl; a.rowmap = rowmap;
   a.heads = (int)heads; a.banks = (int)(batch * heads); a.n_tokens = (int)n_tokens;
   a.rows = (int)g.rows;

@@ -15,14 +15,20 @@
 // restore of recap/operator.py:496-498, 527 are fused into the loads and stores.
 //
 // Epilogues:
-//   head   (oh fp32, lh) in reordered order -- the head branch a refresh capture needs;
+//   head   (oh, lh) in reordered order, oh rounded to the query type as the external
+//          kernel's bf16 output is -- the head branch a refresh capture needs;
 //   dense  output + LSE in native order -- a refresh's dense call;
 //   dense-head  both of a refresh in one pass: the kept blocks are walked first, the head
-//          branch is stored when they are done (bit-identical to the head mode's result),
-//          then the remaining blocks complete the dense output;
+//          branch is stored when they are done, then the remaining blocks complete the
+//          dense output;
 //   merge  head (+) [coarse tail + drift-weighted refinement] in LSE space for rows < R,
 //          the head alone above (recap/kernels/detail_cache.py:220-301), written in
-//          native order: the whole corrected sparse output in one pass.
+//          native order: the whole corrected sparse output in one pass.  The head enters
+//          the merge rounded to the query type, as the reference's head tensor does.
+// The masked modes walk their kept blocks in one order (a kept ragged last block first,
+// then ascending), and dense-head stores its head branch before the first block after the
+// kept ones can move the running max, so the head branch of head, dense-head and merge
+// modes is the same bit for bit.
 #include <type_traits>
 
 #include "kernels.hpp"
@@ -68,16 +74,17 @@ __device__ inline void store_rows(const AttnArgs& a, int bank, int b, int h, int
   const float lse = (m + log2f(lt)) * kLn2;
 
   if constexpr (MODE == kModeHead) {
-    // fp32 head branch: the capture and the merge then see the same unrounded values.
-    float* orow = a.head_out + ((int64_t)bank * a.n_tokens + r) * D;
+    // Head branch in the query type (the reference's head is the bf16 tensor its attention
+    // kernel returns, recap/operator.py:366-370); the capture reads it back from here.
+    uint16_t* orow = a.head_out + ((int64_t)bank * a.n_tokens + r) * D;
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
         const int d0 = 32 * dt + 8 * q4 + 4 * g;
-        *reinterpret_cast<f32x4*>(orow + d0) =
-            f32x4{oacc[dt][4 * q4] * inv, oacc[dt][4 * q4 + 1] * inv,
-                  oacc[dt][4 * q4 + 2] * inv, oacc[dt][4 * q4 + 3] * inv};
+        u32x2 v = {pack2<T>(oacc[dt][4 * q4] * inv, oacc[dt][4 * q4 + 1] * inv),
+                   pack2<T>(oacc[dt][4 * q4 + 2] * inv, oacc[dt][4 * q4 + 3] * inv)};
+        *reinterpret_cast<u32x2*>(orow + d0) = v;
       }
     if (g == 0) a.head_lse[(int64_t)bank * a.n_tokens + r] = lse;
     return;
@@ -99,8 +106,9 @@ __device__ inline void store_rows(const AttnArgs& a, int bank, int b, int h, int
   }
 
   // Merge epilogue (recap/kernels/detail_cache.py:228-301): rows < R get the drift-weighted
-  // tail.  The head output is never materialised here, so it enters in fp32 (the reference
-  // rounds it to bf16 only because its attention kernel stores a bf16 tensor).
+  // tail.  The head is rounded to the query type first: the reference merges the head
+  // tensor its attention kernel stored in that type (recap/operator.py:500-509, loaded with
+  // .to(float32) at recap/kernels/detail_cache.py:228-234).
   if (r < a.rows) {
     const int64_t ri = (int64_t)bank * a.rows + r;
     const float glv = a.gl[ri], dlv = a.dl[ri];
@@ -125,13 +133,15 @@ __device__ inline void store_rows(const AttnArgs& a, int bank, int b, int h, int
         const int d0 = 32 * dt + 8 * q4 + 4 * g;
         const u32x2 gw = *reinterpret_cast<const u32x2*>(gorow + d0);
         const u32x2 dw = *reinterpret_cast<const u32x2*>(drow + d0);
+        const u32x2 hw = {pack2<T>(oacc[dt][4 * q4] * inv, oacc[dt][4 * q4 + 1] * inv),
+                          pack2<T>(oacc[dt][4 * q4 + 2] * inv, oacc[dt][4 * q4 + 3] * inv)};
         float res[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const unsigned gword = gw[e >> 1], dword = dw[e >> 1];
+          const unsigned gword = gw[e >> 1], dword = dw[e >> 1], hword = hw[e >> 1];
           const float gov = T::to_f((uint16_t)((e & 1) ? gword >> 16 : gword & 0xffff));
           const float detv = f16_to_f((uint16_t)((e & 1) ? dword >> 16 : dword & 0xffff));
-          const float ohv = oacc[dt][4 * q4 + e] * inv;
+          const float ohv = T::to_f((uint16_t)((e & 1) ? hword >> 16 : hword & 0xffff));
           const float to = (gov * sm + (gov + detv) * cm) / den;
           res[e] = (ohv * wh + to * wt) / den2;
         }
@@ -242,8 +252,10 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
     int pos = scan[t] - cnt;
     nkeep = __builtin_amdgcn_readfirstlane(scan[kThreads - 1]);
     int npos = nkeep + (j0 - pos);  // blocks not kept before this thread's range
-    // Dense-head mode puts a kept ragged last block first, so its masked steps open the walk.
-    const bool lead = MODE == kModeDenseHead && (a.n_tokens % kBlock) != 0 && mrow[a.tb - 1] != 0;
+    // A kept ragged last block goes first, so its masked steps open the walk (in dense-head
+    // mode the blocks that are not kept follow the kept ones, and the ragged block would
+    // otherwise fall in the middle); every masked mode uses the same order.
+    const bool lead = (a.n_tokens % kBlock) != 0 && mrow[a.tb - 1] != 0;
     for (int j = j0; j < j1; ++j) {
       if (mrow[j]) {
         list[lead ? (j == a.tb - 1 ? 0 : pos + 1) : pos] = j;
@@ -366,6 +378,21 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
     }
   };
 
+  // Dense-head mode: the head branch of the kept blocks (the list's first 2 * nkeep
+  // sub-tiles), stored from the running state once their last PV is done and before the
+  // next sub-tile's scores may raise the running max -- the state head mode ends with.
+  const int kept_end = 2 * nkeep;
+  auto store_head = [&]() __attribute__((always_inline)) {
+    if constexpr (MODE == kModeDenseHead) {
+#pragma unroll
+      for (int q = 0; q < kGroups; ++q) {
+        const float lt = pair_sum(lsum[q]);
+        if (valid[q])
+          store_rows<T, D, kModeHead>(a, bank, b, h, row[q], nat[q], g, oacc[q], m[q], lt);
+      }
+    }
+  };
+
   // One pipeline step, written as slices that the scheduler may not reorder: slice n reads
   // one LDS fragment (of slice n+2) and issues one MFMA per query group with the fragment
   // of slice n -- first the 2*NS of S_{it+1} (head-dimension chunk n/2, key tile n%2),
@@ -387,7 +414,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
     constexpr int NPV = 4 * NDT;             // PV fragments
     constexpr int NN = NQK + NPV;
     constexpr int NPAIR = 16 * kGroups;      // P pairs (16 per group)
-    constexpr int PPS = kNext ? (NPAIR + NQK - 1) / NQK : NPAIR;  // P pairs per slice
+    constexpr int PPS = kNext ? (NPAIR + NQK - 1) / (kNext ? NQK : 1) : NPAIR;  // P pairs per slice
     constexpr int MPS = 16 * kGroups / NPV;  // score pairs of the row max per PV slice
     auto frag = [&](int n) -> u32x4 {
       if (n < NQK) return lds_load16(kl, G::k_off(32 * (n & 1) + l32, 2 * (n >> 1) + g));
@@ -451,9 +478,13 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int q = 0; q < kGroups; ++q) {
-      lsum[q] += part[q][0] + part[q][1];
-      if constexpr (kNext) update_max(q, mx[q]);
+    for (int q = 0; q < kGroups; ++q) lsum[q] += part[q][0] + part[q][1];
+    if constexpr (MODE == kModeDenseHead) {
+      if (it + 1 == kept_end) store_head();
+    }
+    if constexpr (kNext) {
+#pragma unroll
+      for (int q = 0; q < kGroups; ++q) update_max(q, mx[q]);
     }
     tile_barrier();
   };
@@ -472,52 +503,34 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
   }
   using F = std::false_type;
   using Tr = std::true_type;
-  // Dense-head mode: the head branch of the kept blocks (the list's first 2 * nkeep
-  // sub-tiles), stored from the running state once their last PV is done.
-  const int kept_end = 2 * nkeep;
-  auto snapshot = [&](int done) __attribute__((always_inline)) {
-    if constexpr (MODE == kModeDenseHead) {
-      if (done == kept_end) {
-#pragma unroll
-        for (int q = 0; q < kGroups; ++q) {
-          const float lt = pair_sum(lsum[q]);
-          if (valid[q])
-            store_rows<T, D, kModeHead>(a, bank, b, h, row[q], nat[q], g, oacc[q], m[q], lt);
-        }
-      }
-    }
-  };
   // Steps go in pairs (even step: S in sa -> sb, odd step: sb -> sa) so each array keeps one
   // role.  Step it computes S of sub-tile it + 1, masked when that sub-tile lies in the ragged
-  // last block: only the last two pairs (the ragged block last) and, in dense-head mode, the
-  // first pair (a kept ragged block goes first) can meet it, so those are peeled and the main
-  // loop runs unmasked.  The final step has no next sub-tile.
-  snapshot(0);
+  // last block: in the masked modes a kept ragged block goes first (sub-tiles 0 and 1), and in
+  // dense mode, or in dense-head mode when the mask drops it, the ragged block goes last, so
+  // only the first and the last two pairs are peeled and the main loop runs unmasked.  The
+  // final step has no next sub-tile.
+  if (MODE == kModeDenseHead && kept_end == 0) store_head();
   int it = 0;
-  if constexpr (MODE == kModeDenseHead) {
+  if constexpr (MODE != kModeDense) {
     if (nsub >= 4) {
       if (ragged_at(1)) step(0, sa, sb, Tr{}, Tr{}, F{}); else step(0, sa, sb, F{}, Tr{}, F{});
       if (ragged_at(2)) step(1, sb, sa, Tr{}, Tr{}, Tr{}); else step(1, sb, sa, F{}, Tr{}, Tr{});
-      snapshot(2);
       it = 2;
     }
   }
   for (; it + 4 < nsub; it += 2) {
     step(it, sa, sb, F{}, Tr{}, F{});
     step(it + 1, sb, sa, F{}, Tr{}, Tr{});
-    snapshot(it + 2);
   }
   if (nsub - it >= 4) {
     step(it, sa, sb, F{}, Tr{}, F{});
     if (ragged_at(it + 2)) step(it + 1, sb, sa, Tr{}, Tr{}, Tr{});
     else step(it + 1, sb, sa, F{}, Tr{}, Tr{});
-    snapshot(it + 2);
     it += 2;
   }
   if (nsub >= 2) {
     if (ragged_at(it + 1)) step(it, sa, sb, Tr{}, Tr{}, F{}); else step(it, sa, sb, F{}, Tr{}, F{});
     step(it + 1, sb, sa, F{}, F{}, Tr{});
-    snapshot(nsub);
   }
 
   constexpr int kStore = MODE == kModeDenseHead ? kModeDense : MODE;

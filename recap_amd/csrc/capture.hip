@@ -31,16 +31,14 @@ __global__ __launch_bounds__(256) void capture_kernel(CaptureArgs a) {
   const float den = 1.0f - ratio;
 
   const u32x4 ofw = *reinterpret_cast<const u32x4*>(a.of + b * a.osB + h * a.osH + (int64_t)nat * a.osN + 8 * c);
-  const float* ohp = a.oh + ((int64_t)bank * a.n_tokens + r) * D + 8 * c;
-  const f32x4 oh0 = *reinterpret_cast<const f32x4*>(ohp);
-  const f32x4 oh1 = *reinterpret_cast<const f32x4*>(ohp + 4);
+  const u32x4 ohw = *reinterpret_cast<const u32x4*>(a.oh + ((int64_t)bank * a.n_tokens + r) * D + 8 * c);
   const u32x4 gow = *reinterpret_cast<const u32x4*>(a.go + ri * D + 8 * c);
   float of[8], oh[8], go[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const int sh = (e & 1) * 16;
     of[e] = T::to_f((uint16_t)(ofw[e >> 1] >> sh));
-    oh[e] = e < 4 ? oh0[e] : oh1[e - 4];
+    oh[e] = T::to_f((uint16_t)(ohw[e >> 1] >> sh));
     go[e] = T::to_f((uint16_t)(gow[e >> 1] >> sh));
   }
 

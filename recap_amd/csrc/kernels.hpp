@@ -100,7 +100,8 @@ struct AttnArgs {
   int heads, banks, n_tokens, tb;
   int ds;                                        // first long (dense) query row, started first
   float scale_log2;
-  float* head_out; float* head_lse;              // head / dense-head, reordered [bank][N](D), fp32
+  uint16_t* head_out; float* head_lse;           // head / dense-head, reordered [bank][N](D),
+                                                 // head_out in the query type
   uint16_t* out; int64_t osB, osH, osN;          // dense / dense-head / merge, native order
   float* lse_native;                             // dense / dense-head [bank][N]
   int rows; const uint16_t* go; const float* gl; const uint16_t* det; const float* dl;
@@ -117,7 +118,7 @@ hipError_t run_zero_words(unsigned* p, int n, hipStream_t s);
 struct CaptureArgs {
   const uint16_t* of; int64_t osB, osH, osN;     // dense output, native order
   const float* lf;                               // dense LSE, native [bank][N]
-  const float* oh; const float* lh;              // head branch fp32, reordered [bank][N](D)
+  const uint16_t* oh; const float* lh;           // head branch (query type), reordered [bank][N](D)
   const uint16_t* go; const float* gl;           // coarse branch [bank][rows](D)
   const int32_t* rowmap;
   int heads, banks, n_tokens, rows;

@@ -335,10 +335,10 @@ def drift_center(part: torch.Tensor, geo: Geometry) -> torch.Tensor:
 
 def block_sparse_attn(q: torch.Tensor, kv: PackedKV, rowmap: torch.Tensor,
                       kernel_mask: torch.Tensor, geo: Geometry, scale: float):
-    """Head branch (reordered order): (out [banks, N, d] fp32, lse [banks, N])."""
+    """Head branch (reordered order): (out [banks, N, d] in the query dtype, lse [banks, N])."""
     b, h, n, d = q.shape
     kernel_mask = kernel_mask.contiguous()
-    out = torch.empty(b * h, n, d, dtype=torch.float32, device=q.device)
+    out = torch.empty(b * h, n, d, dtype=q.dtype, device=q.device)
     lse = torch.empty(b * h, n, dtype=torch.float32, device=q.device)
     call("recap_block_sparse_attn", *_qkv_args(q), kv.k_tiles.data_ptr(), kv.vt_tiles.data_ptr(),
          rowmap.data_ptr(), kernel_mask.data_ptr(), n, float(scale), out.data_ptr(),
@@ -371,15 +371,15 @@ def dense_head_attn(q: torch.Tensor, kv: PackedKV, rowmap: torch.Tensor,
                     kernel_mask: torch.Tensor, scale: float, out: torch.Tensor | None = None,
                     balance: bool = True):
     """A refresh's dense attention and head branch in one pass:
-    (out [B, H, N, d] native, lse [B, H, N], head_out [banks, N, d] fp32 reordered,
-    head_lse [banks, N]).  `balance` lets XCDs that finish early take the others' last query
+    (out [B, H, N, d] native, lse [B, H, N], head_out [banks, N, d] reordered in the query
+    dtype, head_lse [banks, N]).  `balance` lets XCDs that finish early take the others' last query
     blocks (same outputs)."""
     b, h, n, d = q.shape
     kernel_mask = kernel_mask.contiguous()
     if out is None:
         out = torch.empty(b, h, n, d, dtype=q.dtype, device=q.device)
     lse = torch.empty(b, h, n, dtype=torch.float32, device=q.device)
-    head_out = torch.empty(b * h, n, d, dtype=torch.float32, device=q.device)
+    head_out = torch.empty(b * h, n, d, dtype=q.dtype, device=q.device)
     head_lse = torch.empty(b * h, n, dtype=torch.float32, device=q.device)
     call("recap_dense_head_attn", *_qkv_args(q), kv.k_tiles.data_ptr(), kv.vt_tiles.data_ptr(),
          rowmap.data_ptr(), kernel_mask.data_ptr(), n, float(scale), out.data_ptr(),
@@ -420,6 +420,8 @@ def refresh_capture(dense_out: torch.Tensor, dense_lse: torch.Tensor, head_out: 
     b, h, n, d = dense_out.shape
     if not all(t.is_contiguous() for t in (dense_lse, head_out, head_lse, go, gl, det, dl)):
         raise ValueError("capture inputs must be contiguous")
+    if head_out.dtype != dense_out.dtype or go.dtype != dense_out.dtype:
+        raise ValueError("capture: head and coarse outputs must have the dense output's dtype")
     stats = part = None
     if glref is not None:
         npart = int(_lib.load().recap_capture_partials(b * h, d, geo.n_video))

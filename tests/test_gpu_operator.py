@@ -8,7 +8,7 @@ import pytest
 import torch
 
 import oracle as O
-from gpu_util import SMALL, assert_close_bf16, bf16_tolerance, metrics
+from gpu_util import (SMALL, assert_parity, assert_sparse_parity, metrics, parity_tolerance)
 from recap_amd import HostBankOperator, Operator, OperatorConfig, REFRESH, SPARSE
 from recap_amd.layout import Layout, SparseGeometry, hilbert_permutation
 from recap_amd.synthetic import WORKLOADS, make_qkv, perturb
@@ -43,8 +43,8 @@ def test_refresh_sparse_sequence_vs_oracle(cuda, name):
     """REFRESH / SPARSE / REFRESH (revalidation) / SPARSE against the oracle operator.
 
     Each sparse call is compared on the same refinement state (the GPU's state is handed to
-    the oracle after every refresh) with the oracle's unrounded fp32 output as reference:
-    the hot path must then agree within max-abs 2e-2 and cosine 0.999."""
+    the oracle after every refresh): every output element within max-abs 2e-2 of the
+    oracle's bf16 output (one bf16 ulp where that is larger) and cosine >= 0.999."""
     wl = SMALL[name]
     print(f"case {name}", flush=True)
     q, k, v = make_qkv(wl, seed=0)
@@ -54,7 +54,7 @@ def test_refresh_sparse_sequence_vs_oracle(cuda, name):
     op.begin_step(0, REFRESH)
     out = op.attend(0, g(q), g(k), g(v))
     ref.refresh(0, q, k, v)
-    assert_close_bf16(out.cpu().float(), ref.last["out_f32"], f"refresh-0 {name}")
+    assert_parity(out.cpu().float(), ref.last["out_f32"], f"refresh-0 {name}")
     bank = op.banks[0][0]
     assert torch.equal(bank.partition.cpu().reshape(ref.layers[0].partition.shape),
                        ref.layers[0].partition)
@@ -63,12 +63,12 @@ def test_refresh_sparse_sequence_vs_oracle(cuda, name):
     op.begin_step(1, SPARSE)
     out = op.attend(0, g(q1), g(k1), g(v1))
     ref.sparse(0, q1, k1, v1)
-    assert_close_bf16(out.cpu().float(), ref.last["out_f32"], f"sparse-1 {name}")
+    assert_sparse_parity(out, ref, op, q1, k1, v1, wl, cuda, f"sparse-1 {name}")
     q2, k2, v2 = (perturb(x, 0.03, seed=1, step=2) for x in (q, k, v))
     op.begin_step(2, REFRESH)
     out = op.attend(0, g(q2), g(k2), g(v2))
     ref.refresh(0, q2, k2, v2)
-    assert_close_bf16(out.cpu().float(), ref.last["out_f32"], f"refresh-2 {name}")
+    assert_parity(out.cpu().float(), ref.last["out_f32"], f"refresh-2 {name}")
     age, error = op.drain_validation()
     num, den = (float(x) for x in ref.layers[0].pending_stats)
     print(f"  validation error gpu={error:.5f} oracle={math.sqrt(num / den):.5f} "
@@ -79,7 +79,7 @@ def test_refresh_sparse_sequence_vs_oracle(cuda, name):
     op.begin_step(3, SPARSE)
     out = op.attend(0, g(q3), g(k3), g(v3))
     ref.sparse(0, q3, k3, v3)
-    assert_close_bf16(out.cpu().float(), ref.last["out_f32"], f"sparse-3 {name}")
+    assert_sparse_parity(out, ref, op, q3, k3, v3, wl, cuda, f"sparse-3 {name}")
 
 
 @pytest.mark.parametrize("name,dtype,batch", [
@@ -98,14 +98,16 @@ def test_fp16_and_batched_calls_vs_oracle(cuda, name, dtype, batch):
     out = op.attend(0, g(q), g(k), g(v))
     assert out.dtype == dtype and out.shape == q.shape
     ref.refresh(0, q, k, v, dtype=dtype)
-    assert_close_bf16(out.cpu().float(), ref.last["out_f32"], f"refresh {name} {dtype} b{batch}")
+    assert_parity(out.cpu().float(), ref.last["out_f32"], f"refresh {name} {dtype} b{batch}",
+                  dtype=dtype)
     inject(ref, op, 0, wl)
     q1, k1, v1 = (perturb(x, 0.02, seed=4, step=1) for x in (q, k, v))
     op.begin_step(1, SPARSE)
     out = op.attend(0, g(q1), g(k1), g(v1))
     assert out.dtype == dtype
     ref.sparse(0, q1, k1, v1, dtype=dtype)
-    assert_close_bf16(out.cpu().float(), ref.last["out_f32"], f"sparse {name} {dtype} b{batch}")
+    assert_sparse_parity(out, ref, op, q1, k1, v1, wl, cuda, f"sparse {name} {dtype} b{batch}",
+                         dtype=dtype)
 
 
 @pytest.mark.parametrize("name", list(SMALL))
@@ -127,7 +129,8 @@ def test_sparse_vs_oracle_with_independent_state(cuda, name):
     ref.sparse(0, q1, k1, v1)
     want = ref.last["out_f32"]
     m, c = metrics(out, want)
-    frac = float(((out - want).abs() > bf16_tolerance(out, want)).float().mean())
+    frac = float(((out - want.to(torch.bfloat16).float()).abs()
+                  > parity_tolerance(want)).float().mean())
     print(f"[independent {name}] max_abs={m:.3e} cos={c:.6f} frac-beyond-tolerance={frac:.2e}",
           flush=True)
     assert c >= 0.999 and frac <= 1e-3 and m < 0.25
@@ -146,7 +149,7 @@ def test_alpha_override_knob_vs_oracle(cuda):
     op.begin_step(1, SPARSE)
     out = op.attend(0, q1.to(cuda), k1.to(cuda), v1.to(cuda))
     ref.sparse(0, q1, k1, v1, alpha_override=0.8)
-    assert_close_bf16(out.cpu().float(), ref.last["out_f32"], "alpha=0.8")
+    assert_sparse_parity(out, ref, op, q1, k1, v1, wl, cuda, "alpha=0.8", alpha_override=0.8)
 
 
 def test_sparse_before_refresh_raises(cuda):
@@ -179,7 +182,7 @@ def test_non_contiguous_inputs_and_exact_kind(cuda):
     assert torch.equal(op.attend(0, q, k, v), op2.attend(0, qt, kt, vt))
     op.begin_step(2, "exact")
     exact = op.attend(0, q, k, v)
-    assert_close_bf16(exact.float(), a.float(), "exact vs refresh dense")
+    assert_parity(exact.float(), a.float(), "exact vs refresh dense")
 
 
 # -- full HunyuanVideo-720p shape: size-independent properties ----------------------------
@@ -247,7 +250,7 @@ def test_full_length_refresh_and_sparse_vs_oracle(cuda, name, heads):
     op.begin_step(0, REFRESH)
     out = op.attend(0, g(q), g(k), g(v))
     ref.refresh(0, q, k, v)
-    assert_close_bf16(out.cpu().float(), ref.last["out_f32"], f"refresh {name}")
+    assert_parity(out.cpu().float(), ref.last["out_f32"], f"refresh {name}")
     print(f"  refresh {name}: oracle done, outputs agree", flush=True)
     bank = op.banks[0][0]
     assert torch.equal(bank.partition.cpu().reshape(ref.layers[0].partition.shape),
@@ -258,28 +261,7 @@ def test_full_length_refresh_and_sparse_vs_oracle(cuda, name, heads):
     got = op.attend(0, g(q1), g(k1), g(v1)).cpu().double()
     ref.sparse(0, q1, k1, v1)
     want = ref.last["out_f32"].double()
-    # The coarse tail's gate [fl(s^2 qsq.w) <= theta^2] is discontinuous: a row with an
-    # omitted block within fp32 rounding of the threshold may take either decision in any
-    # two implementations (they sum qsq.w in different orders).  Every element of the other
-    # rows must meet the bf16 bound; the few borderline rows are reported.
-    ctx, state = ref.last["ctx"], ref.layers[0]
-    margin = O.gate_margin(ctx["qsq"], ctx["w"], state.partition, 1.0 / math.sqrt(wl.dim),
-                           2.0, wl.video_tokens, torch.bfloat16)
-    rows = torch.cat([margin, torch.full((margin.shape[0], wl.text_tokens), math.inf,
-                                         dtype=torch.float64)], dim=1)
-    native = O.restore(rows.unsqueeze(-1), ref.inv).squeeze(-1).reshape(1, heads, wl.tokens, 1)
-    borderline = native < 1e-5
-    m, c = metrics(got, want)
-    excess = (got - want).abs() - bf16_tolerance(got, want)
-    clean = float(excess.masked_fill(borderline, -math.inf).max())
-    worst = float(excess.max())
-    print(f"[sparse {name}] max_abs={m:.3e} cos={c:.6f} worst-vs-tolerance={worst:+.3e} "
-          f"outside borderline rows={clean:+.3e} borderline rows={int(borderline.sum())} of "
-          f"{heads * wl.tokens}", flush=True)
-    assert c >= 0.999 and clean <= 0
-    # The exclusion must stay small: ~1e-5 of threshold width times a few hundred omitted
-    # blocks per row puts 0.1-0.3% of rows within it.
-    assert int(borderline.sum()) <= heads * wl.tokens // 100
+    assert_sparse_parity(got, ref, op, q1, k1, v1, wl, cuda, f"sparse {name}")
 
 
 @pytest.fixture(scope="module")
@@ -295,10 +277,10 @@ def test_hunyuan_refresh_then_sparse_reproduces_dense(hunyuan_inputs):
     op.begin_step(0, REFRESH)
     dense = op.attend(0, q, k, v)
     ref = torch.nn.functional.scaled_dot_product_attention(q[:, :2], k[:, :2], v[:, :2])
-    assert_close_bf16(dense[:, :2].float(), ref.float(), "hunyuan dense vs sdpa (2 heads)")
+    assert_parity(dense[:, :2].float(), ref.float(), "hunyuan dense vs sdpa (2 heads)")
     op.begin_step(1, SPARSE)
     sparse = op.attend(0, q, k, v)
-    assert_close_bf16(sparse.float(), dense.float(), "hunyuan refresh->sparse == dense")
+    assert_parity(sparse.float(), dense.float(), "hunyuan refresh->sparse == dense")
 
 
 def test_hunyuan_bank_chunks_and_host_banks_are_identical(hunyuan_inputs):

@@ -1,7 +1,8 @@
 """GPU parity of each HIP stage against the CPU oracle, on the same seeded inputs.
 
-Masks, pooled means and block scores must be bit-exact; bf16 outputs within max-abs
-2e-2 and cosine >= 0.999; fp32 statistics within the tolerance stated per test."""
+Masks, pooled means and block scores must be bit-exact; bf16 outputs within max-abs 2e-2
+of the oracle's output rounded to bf16 (one bf16 ulp where that is larger, |x| >= 4) and
+cosine >= 0.999; fp32 statistics within the tolerance stated per test."""
 
 import math
 
@@ -10,7 +11,7 @@ import pytest
 import torch
 
 import oracle as O
-from gpu_util import (SMALL, assert_close_bf16, banks_view, k_tile_to_rows, metrics,
+from gpu_util import (SMALL, assert_parity, banks_view, k_tile_to_rows, metrics,
                       scale_for, vt_tile_to_rows)
 from recap_amd import _lib
 from recap_amd import kernels as K
@@ -91,14 +92,14 @@ def test_head_and_dense_attention(cuda, name):
     kmask_ref = O.kernel_block_mask(part_ref, wl.tokens, wl.video_tokens)
     out, lse = K.block_sparse_attn(qg, kv, rowmap, kmask_ref.to(cuda), geo, scale)
     ref, ref_lse = O.block_sparse_attention(ql, kl, vl, kmask_ref, scale)
-    assert_close_bf16(out.cpu().float(), ref, f"head {name}")
+    assert_parity(out.cpu().float(), ref, f"head {name}")
     m, _ = metrics(lse.cpu(), ref_lse)
     assert m < 2e-3, m
     dense, dlse = K.dense_attn(qg, kv, rowmap, scale)
     dref, dref_lse = O.dense_attention(ql, kl, vl, scale)
     _, inv = O.gather_indices(hilbert_permutation(wl.grid), wl.text_tokens, wl.text_first)
     b, h = q.shape[:2]
-    assert_close_bf16(dense.cpu().float(), O.restore(dref.reshape(b, h, -1, wl.dim), inv),
+    assert_parity(dense.cpu().float(), O.restore(dref.reshape(b, h, -1, wl.dim), inv),
                       f"dense {name}")
     m, _ = metrics(dlse.cpu(), dref_lse.reshape(b, h, -1).index_select(-1, inv))
     assert m < 2e-3, m
@@ -117,22 +118,19 @@ def test_dense_head_attention_one_pass(cuda, name):
     kmask_ref = O.kernel_block_mask(part_ref, wl.tokens, wl.video_tokens)
     dense, dlse, hout, hlse = K.dense_head_attn(qg, kv, rowmap, kmask_ref.to(cuda), scale)
     ref, ref_lse = O.block_sparse_attention(ql, kl, vl, kmask_ref, scale)
-    assert_close_bf16(hout.cpu().float(), ref, f"fused head {name}")
+    assert_parity(hout.cpu().float(), ref, f"fused head {name}")
     m, _ = metrics(hlse.cpu(), ref_lse)
     assert m < 2e-3, m
-    # Same kept blocks, but a kept ragged block goes first here and the running max may
-    # also move with the first block after the kept ones: P, rounded to bf16 for the PV
-    # product, is rounded under another max, so the two agree to the bf16 precision of P;
-    # the LSE to fp32 rounding.
+    # Same kept blocks in the same order (a kept ragged block first in both), and the head
+    # branch is stored before the first block after the kept ones can move the running max:
+    # the head branch equals the head kernel's bit for bit.
     alone, alone_lse = K.block_sparse_attn(qg, kv, rowmap, kmask_ref.to(cuda), geo, scale)
-    m, _ = metrics(hout.cpu(), alone.cpu())
-    print(f"  fused head vs head kernel (fp32): max_abs {m:.2e}", flush=True)
-    assert m < 2e-2
-    assert float((hlse - alone_lse).abs().max()) < 1e-4
+    assert torch.equal(hout, alone)
+    assert torch.equal(hlse, alone_lse)
     dref, dref_lse = O.dense_attention(ql, kl, vl, scale)
     _, inv = O.gather_indices(hilbert_permutation(wl.grid), wl.text_tokens, wl.text_first)
     b, h = q.shape[:2]
-    assert_close_bf16(dense.cpu().float(), O.restore(dref.reshape(b, h, -1, wl.dim), inv),
+    assert_parity(dense.cpu().float(), O.restore(dref.reshape(b, h, -1, wl.dim), inv),
                       f"fused dense {name}")
     m, _ = metrics(dlse.cpu(), dref_lse.reshape(b, h, -1).index_select(-1, inv))
     assert m < 2e-3, m
@@ -144,8 +142,9 @@ def test_dense_head_attention_one_pass(cuda, name):
 @pytest.mark.parametrize("n,d,keep_last", [(100, 64, True), (200, 128, True), (200, 128, False),
                                           (300, 64, False), (384, 128, True), (700, 128, False)])
 def test_attention_modes_short_and_ragged(cuda, n, d, keep_last):
-    """Head, dense and dense-head modes on one to six blocks, with the ragged last block kept
-    (walked first in dense-head mode) or not kept (walked last), against the oracle."""
+    """Head, dense, dense-head and merge modes on one to six blocks, with the ragged last
+    block kept (walked first) or not kept (walked last in dense-head mode), against the
+    oracle."""
     print(f"case n={n} d={d} keep_last={keep_last}", flush=True)
     g = torch.Generator().manual_seed(n + d)
     banks, tb = 2, -(-n // 128)
@@ -163,12 +162,20 @@ def test_attention_modes_short_and_ragged(cuda, n, d, keep_last):
     ref, ref_lse = O.block_sparse_attention(ql, kl, vl, kmask, scale)
     dref, dref_lse = O.dense_attention(ql, kl, vl, scale)
     head, head_lse = K.block_sparse_attn(q.to(cuda), kv, rowmap, kmask.to(cuda), geo, scale)
-    assert_close_bf16(head.cpu().float(), ref, "head")
+    assert_parity(head.cpu().float(), ref, "head")
     dense, dlse = K.dense_attn(q.to(cuda), kv, rowmap, scale)
-    assert_close_bf16(dense.cpu().float()[0], dref, "dense")
+    assert_parity(dense.cpu().float()[0], dref, "dense")
     fd, flse, fh, fhlse = K.dense_head_attn(q.to(cuda), kv, rowmap, kmask.to(cuda), scale)
-    assert_close_bf16(fh.cpu().float(), ref, "dense-head: head")
-    assert_close_bf16(fd.cpu().float()[0], dref, "dense-head: dense")
+    assert_parity(fh.cpu().float(), ref, "dense-head: head")
+    assert_parity(fd.cpu().float()[0], dref, "dense-head: dense")
+    # One walk order for every masked mode: the head branch of the dense-head pass and the
+    # head the merge epilogue uses are the head kernel's, bit for bit.  With fewer than 128
+    # video tokens no row is refined (R = 0), so the merge output is the head itself.
+    assert torch.equal(fh, head) and torch.equal(fhlse, head_lse)
+    merged = K.sparse_merge_attn(q.to(cuda), kv, rowmap, kmask.to(cuda),
+                                 K.Geometry(n, min(n, 100)), scale, None, None, None, None,
+                                 None, None)
+    assert torch.equal(merged[0], head)
     for got, want in ((head_lse, ref_lse), (fhlse, ref_lse), (dlse[0], dref_lse),
                       (flse[0], dref_lse)):
         m, _ = metrics(got.cpu(), want)
@@ -185,7 +192,7 @@ def test_dense_attention_matches_torch_sdpa(cuda):
     kv = K.kv_pack(k, v, rowmap, geo)
     out, _ = K.dense_attn(q, kv, rowmap, scale_for(wl.dim))
     ref = torch.nn.functional.scaled_dot_product_attention(q.float(), k.float(), v.float())
-    assert_close_bf16(out.float(), ref, "dense vs sdpa fp32")
+    assert_parity(out.float(), ref, "dense vs sdpa fp32")
 
 
 @pytest.mark.parametrize("name", ["tiny", "text-last-d128", "video-ragged-d128"])
@@ -249,7 +256,7 @@ def test_coarse_tail(cuda, name, rank):
               "rank": rank}
     glref = torch.randn(kl.shape[0], rows, generator=torch.Generator().manual_seed(3)).to(cuda)
     go, gl, dpart = K.coarse_tail(qg, rowmap, part.to(cuda), geo, tables, scale, 2.0, glref)
-    assert_close_bf16(go.cpu().float(), go_ref[:, :rows], f"coarse {name}")
+    assert_parity(go.cpu().float(), go_ref[:, :rows], f"coarse {name}")
     fin = torch.isfinite(gl_ref[:, :rows])
     assert torch.equal(torch.isfinite(gl.cpu()), fin)
     m, _ = metrics(gl.cpu()[fin], gl_ref[:, :rows][fin])

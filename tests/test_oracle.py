@@ -504,3 +504,117 @@ def test_topk_margin_brute_force():
         gaps.append(top[4] - top[5])
     assert O.topk_margin(s, 5) == pytest.approx(min(gaps), abs=1e-6)
     assert O.topk_margin(s, 20) == float("inf")
+
+
+# -- the validation statistic and the rerank branch of a revalidating refresh ---------------
+
+
+def _refreshed(seed=0, dtype=torch.float32):
+    wl = WORKLOADS["cpu-plumbing"]
+    q, k, v = make_qkv(wl, seed=seed)
+    op = O.OracleOperator(wl.grid, wl.text_tokens, wl.text_first, wl.density)
+    op.refresh(0, q, k, v, dtype=dtype)
+    return op, op.last
+
+
+def _capture_terms(op, last):
+    """Reordered-row views of the refresh's dense output and the ratio of the capture."""
+    rows = last["go"].shape[1]
+    lf = last["full_l"][:, :rows].double()
+    of = last["full_o"][:, :rows].double()
+    oh, go = last["oh"][:, :rows].double(), last["go"].double()
+    lh = last["lh"][:, :rows].double()
+    ratio = torch.clamp_max(torch.exp(torch.clamp_max(lh - lf, 0.0)), 1 - 1e-6)
+    return rows, of, oh, go, lf, ratio
+
+
+def _stats(op, last, det, dl, glref, center):
+    """O.refresh_detail's validation pair for the old refinement (det, dl) with drift
+    inputs (glref, center) on the refresh's own dense output, head and coarse tail."""
+    nat_o = O.restore(last["full_o"], op.inv)
+    nat_l = last["full_l"].index_select(-1, op.inv)
+    _, _, stats = O.refresh_detail(nat_o, nat_l, last["oh"], last["lh"], last["go"], last["gl"],
+                                   op.permutation, op.video_offset,
+                                   (det, dl, glref, center))
+    return stats.double()
+
+
+def test_validation_statistic_closed_forms():
+    """The validation pair sum (old - of)^2, sum of^2 of recap/kernels/detail_cache.py:
+    115-160, against closed forms on a refresh's own inputs.  With DL = lf + ln(1 - r) - gl
+    (unclamped) and head mass e^lh = r e^lf, the old sparse output with drift weight a per
+    row, refinement D' and log-mass DL + delta is
+        [r oh + (1 - a) c go + a e^delta (1 - r)(go + D')] / [r + (1 - a) c + a e^delta (1 - r)]
+    with c = e^(gl - lf) the coarse tail's share of the dense mass."""
+    op, last = _refreshed()
+    state = op.layers[0]
+    rows, of, oh, go, lf, r = _capture_terms(op, last)
+    gl = last["gl"].double()
+    assert bool((state.dl.abs() < 30).all())  # no clamped log-mass in this input
+    c = torch.exp(gl - lf)
+    want_ref2 = float((of ** 2).sum())
+
+    def closed(det, alpha, delta):
+        a = alpha.unsqueeze(-1)
+        rr, cc = r.unsqueeze(-1), c.unsqueeze(-1)
+        num = rr * oh + (1 - a) * cc * go + a * math.exp(delta) * (1 - rr) * (go + det)
+        den = rr + (1 - a) * cc + a * math.exp(delta) * (1 - rr)
+        return float(((num / den - of) ** 2).sum())
+
+    ones = torch.ones_like(gl)
+    zero = torch.zeros(gl.shape[0])
+    # 1. an offset refinement, drift weight 1
+    det1 = state.det + 0.5
+    got = _stats(op, last, det1, state.dl, last["gl"], zero)
+    assert abs(float(got[1]) - want_ref2) <= 1e-6 * want_ref2
+    want = closed(det1.double(), ones, 0.0)
+    assert abs(float(got[0]) - want) <= 1e-4 * want, (float(got[0]), want)
+    # 2. an offset log-mass
+    got = _stats(op, last, state.det, state.dl + 0.3, last["gl"], zero)
+    want = closed(state.det.double(), ones, 0.3)
+    assert abs(float(got[0]) - want) <= 1e-4 * want, (float(got[0]), want)
+    # 3. drift weight below one: the coarse log-mass moved by a row-dependent shift
+    g = torch.Generator().manual_seed(5)
+    shift = 0.7 * torch.randn(gl.shape, generator=g)
+    center = torch.full((gl.shape[0],), 0.1)
+    alpha = torch.exp(-(shift - 0.1).abs()).double()
+    got = _stats(op, last, det1, state.dl, last["gl"] - shift, center)
+    want = closed(det1.double(), alpha, 0.0)
+    assert abs(float(got[0]) - want) <= 1e-4 * want, (float(got[0]), want)
+    # 4. the refinement just captured: what is left is the reference's own rounding, the
+    # fp16 D and the zeroed rows, (1 - r)(D - exact tail + go) per element
+    got = _stats(op, last, state.det, state.dl, last["gl"], zero)
+    exact = (of - r.unsqueeze(-1) * oh) / (1 - r).unsqueeze(-1) - go
+    left = float((((1 - r).unsqueeze(-1) * (state.det.double() - exact)) ** 2).sum())
+    print(f"identity e_detail {math.sqrt(float(got[0]) / want_ref2):.3e} closed form "
+          f"{math.sqrt(left / want_ref2):.3e}")
+    assert abs(math.sqrt(float(got[0])) - math.sqrt(left)) <= 1e-3 * math.sqrt(left) + 1e-6
+
+
+@pytest.mark.parametrize("min_overlap,expect_rerank", [(1.0, True), (0.0, False)])
+def test_rerank_branch_of_a_revalidating_refresh(min_overlap, expect_rerank):
+    """recap/operator.py:414-469: a revalidating refresh selects again; below the overlap
+    threshold the new partition replaces the old one (it is the fresh head_partition of the
+    new inputs) and the refinement is recaptured for it, so a sparse call on the refresh's
+    own inputs reproduces its dense output; at or above the threshold the old split stays."""
+    wl = WORKLOADS["cpu-plumbing"]
+    q, k, v = make_qkv(wl, seed=0)
+    op = O.OracleOperator(wl.grid, wl.text_tokens, wl.text_first, wl.density,
+                          rerank_min_overlap=min_overlap)
+    op.refresh(0, q, k, v, dtype=torch.float32)
+    old = op.layers[0].partition.clone()
+    q2, k2, v2 = (x + 0.4 * torch.randn(x.shape, generator=torch.Generator().manual_seed(i))
+                  for i, x in enumerate((q, k, v)))
+    dense = op.refresh(0, q2, k2, v2, dtype=torch.float32)
+    assert op.layers[0].pending_stats is not None
+    assert op.last["rerank"] is expect_rerank
+    fresh = O.head_partition(O.reorder(q2, op.fwd).reshape(2, -1, 64),
+                             O.reorder(k2, op.fwd).reshape(2, -1, 64), 1 / 8.0, wl.density,
+                             op.n_video)
+    assert not torch.equal(fresh, old)
+    assert torch.equal(op.layers[0].partition, fresh if expect_rerank else old)
+    sparse = op.sparse(0, q2, k2, v2, dtype=torch.float32)
+    err = (sparse - dense).abs()
+    print(f"min_overlap={min_overlap}: sparse vs dense on the refresh inputs max {err.max():.2e}")
+    assert float(op.last["center"].abs().max()) < 1e-6
+    assert float(err.median()) < 1e-5 and float(err.max()) < 2e-2
