@@ -262,6 +262,25 @@ int recap_refresh_capture(const void* dense_out, int dtype, int64_t batch, int64
                           float* dl, const float* glref, const float* center,
                           float* stat_partial, float* stats, void* stream);
 
+/* recap_refresh_capture without a caller workspace: the validation's partial pairs go to
+ * a static device array of RECAP_CAPTURE_NOALLOC_MAX_PAIRS pairs (4 MiB) that each GPU holds
+ * from the first call on it until the process ends; the call allocates nothing.  Same
+ * arguments and results as recap_refresh_capture minus stat_partial; a validation needing
+ * more pairs than recap_capture_partials() allows fails with RECAP_EINVAL.  Every pair the
+ * final sum reads is written by the same call first, so nothing needs clearing; calls that
+ * overlap on one GPU (concurrent streams) race on the array and must be serialised.
+ * No counterpart in the reference: for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops that forbid hipMalloc). */
+#define RECAP_CAPTURE_NOALLOC_MAX_PAIRS (1 << 19)
+int recap_refresh_capture_noalloc(const void* dense_out, int dtype, int64_t batch,
+                                  int64_t heads, int64_t dim, int64_t out_stride_b,
+                                  int64_t out_stride_h, int64_t out_stride_n,
+                                  const float* dense_lse, const void* head_out,
+                                  const float* head_lse, const void* go, const float* gl,
+                                  const int32_t* rowmap, int64_t n_tokens, int64_t n_video,
+                                  void* det, float* dl, const float* glref,
+                                  const float* center, float* stats, void* stream);
+
 /* Asynchronous copy of a refinement bank between pinned host memory and the device on
  * `stream` (hipMemcpyAsync, direction inferred).
  * Replaces the non_blocking copy_ of recap/host_banks.py:99-103. */

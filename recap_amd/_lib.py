@@ -16,6 +16,7 @@ ABI_VERSION = 4
 RECAP_OK, RECAP_EINVAL, RECAP_EUNSUPPORTED, RECAP_EHIP = 0, 1, 2, 3
 RECAP_F16, RECAP_BF16 = 1, 2
 CLOSURE_ROT, CLOSURE_CVK, CLOSURE_SCATTER = 1, 2, 4
+CAPTURE_NOALLOC_MAX_PAIRS = 1 << 19  # RECAP_CAPTURE_NOALLOC_MAX_PAIRS
 
 _P, _I64, _I, _F = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
 _STRIDES = [_I64, _I64, _I64]
@@ -58,6 +59,8 @@ SIGNATURES: dict[str, tuple] = {
     "recap_capture_partials": (_I64, [_I64, _I64, _I64]),
     "recap_refresh_capture": (_I, [_P, _I, _I64, _I64, _I64, *_STRIDES, _P, _P, _P, _P, _P, _P,
                                    _I64, _I64, _P, _P, _P, _P, _P, _P, _P]),
+    "recap_refresh_capture_noalloc": (_I, [_P, _I, _I64, _I64, _I64, *_STRIDES, _P, _P, _P,
+                                           _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P]),
     "recap_bank_copy_async": (_I, [_P, _P, _I64, _P]),
 }
 

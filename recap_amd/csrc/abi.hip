@@ -527,23 +527,22 @@ int64_t recap_capture_partials(int64_t banks, int64_t dim, int64_t n_video) {
   return banks * ((n_video / kBlock) * kBlock / rpb);
 }
 
-int recap_refresh_capture(const void* dense_out, int dtype, int64_t batch, int64_t heads,
-                          int64_t dim, int64_t out_stride_b, int64_t out_stride_h,
-                          int64_t out_stride_n, const float* dense_lse, const void* head_out,
-                          const float* head_lse, const void* go, const float* gl,
-                          const int32_t* rowmap, int64_t n_tokens, int64_t n_video, void* det,
-                          float* dl, const float* glref, const float* center,
-                          float* stat_partial, float* stats, void* stream) {
+// Arguments of a refresh capture, validated; false when there is nothing to do (R = 0).
+static int capture_args(const void* dense_out, int dtype, int64_t batch, int64_t heads,
+                        int64_t dim, int64_t out_stride_b, int64_t out_stride_h,
+                        int64_t out_stride_n, const float* dense_lse, const void* head_out,
+                        const float* head_lse, const void* go, const float* gl,
+                        const int32_t* rowmap, int64_t n_tokens, int64_t n_video, void* det,
+                        float* dl, const float* glref, const float* center, float* stats,
+                        CaptureArgs& a, bool& work) {
   CHECK(check_common(dtype, dim));
   CHECK(check_tokens(n_tokens, n_video));
   CHECK(check_qkv("dense_out", dense_out, batch, heads, out_stride_b, out_stride_h, out_stride_n));
   REQUIRE(dense_lse && head_out && head_lse && go && gl && rowmap && det && dl, "NULL pointer");
   REQUIRE(aligned16(head_out) && aligned16(go) && aligned16(det), "16-byte alignment");
-  const bool validate = glref != nullptr;
-  REQUIRE(!validate || (center && stat_partial && stats), "validation needs center, stat_partial, stats");
+  REQUIRE(glref == nullptr || (center && stats), "validation needs center and stats");
   const Geom g = geometry(n_tokens, n_video);
-  if (g.rows == 0) return RECAP_OK;
-  CaptureArgs a{};
+  work = g.rows > 0;
   a.of = static_cast<const uint16_t*>(dense_out);
   a.osB = out_stride_b; a.osH = out_stride_h; a.osN = out_stride_n;
   a.lf = dense_lse; a.oh = static_cast<const uint16_t*>(head_out); a.lh = head_lse;
@@ -551,11 +550,63 @@ int recap_refresh_capture(const void* dense_out, int dtype, int64_t batch, int64
   a.heads = (int)heads; a.banks = (int)(batch * heads); a.n_tokens = (int)n_tokens;
   a.rows = (int)g.rows;
   a.det = static_cast<uint16_t*>(det); a.dl = dl;
-  a.glref = glref; a.center = center; a.stat_part = stat_partial;
+  a.glref = glref; a.center = center;
+  return RECAP_OK;
+}
+
+int recap_refresh_capture(const void* dense_out, int dtype, int64_t batch, int64_t heads,
+                          int64_t dim, int64_t out_stride_b, int64_t out_stride_h,
+                          int64_t out_stride_n, const float* dense_lse, const void* head_out,
+                          const float* head_lse, const void* go, const float* gl,
+                          const int32_t* rowmap, int64_t n_tokens, int64_t n_video, void* det,
+                          float* dl, const float* glref, const float* center,
+                          float* stat_partial, float* stats, void* stream) {
+  CaptureArgs a{};
+  bool work = false;
+  CHECK(capture_args(dense_out, dtype, batch, heads, dim, out_stride_b, out_stride_h,
+                     out_stride_n, dense_lse, head_out, head_lse, go, gl, rowmap, n_tokens,
+                     n_video, det, dl, glref, center, stats, a, work));
+  const bool validate = glref != nullptr;
+  REQUIRE(!validate || stat_partial, "validation needs stat_partial");
+  if (!work) return RECAP_OK;
+  a.stat_part = stat_partial;
   int blocks = 0;
   hipStream_t s = as_stream(stream);
   CHECK(hip_status(run_capture(a, dtype, (int)dim, &blocks, s), "capture launch"));
   if (validate) CHECK(hip_status(run_sum_pairs(stat_partial, a.banks * blocks, stats, s), "sum_pairs launch"));
+  return RECAP_OK;
+}
+
+int recap_refresh_capture_noalloc(const void* dense_out, int dtype, int64_t batch,
+                                  int64_t heads, int64_t dim, int64_t out_stride_b,
+                                  int64_t out_stride_h, int64_t out_stride_n,
+                                  const float* dense_lse, const void* head_out,
+                                  const float* head_lse, const void* go, const float* gl,
+                                  const int32_t* rowmap, int64_t n_tokens, int64_t n_video,
+                                  void* det, float* dl, const float* glref,
+                                  const float* center, float* stats, void* stream) {
+  CaptureArgs a{};
+  bool work = false;
+  CHECK(capture_args(dense_out, dtype, batch, heads, dim, out_stride_b, out_stride_h,
+                     out_stride_n, dense_lse, head_out, head_lse, go, gl, rowmap, n_tokens,
+                     n_video, det, dl, glref, center, stats, a, work));
+  const bool validate = glref != nullptr;
+  if (validate) {
+    const int64_t pairs = recap_capture_partials(batch * heads, dim, n_video);
+    static_assert(kCaptureScratchPairs == RECAP_CAPTURE_NOALLOC_MAX_PAIRS, "scratch size");
+    REQUIRE(pairs <= kCaptureScratchPairs,
+            "validation needs %lld partial pairs; the static scratch holds %lld (4 MiB): use "
+            "recap_refresh_capture with a caller workspace",
+            (long long)pairs, (long long)kCaptureScratchPairs);
+  }
+  if (!work) return RECAP_OK;
+  float* scratch = nullptr;
+  if (validate) CHECK(hip_status(capture_scratch_pointer(&scratch), "static scratch lookup"));
+  a.stat_part = scratch;
+  int blocks = 0;
+  hipStream_t s = as_stream(stream);
+  CHECK(hip_status(run_capture(a, dtype, (int)dim, &blocks, s), "capture launch"));
+  if (validate) CHECK(hip_status(run_sum_pairs(scratch, a.banks * blocks, stats, s), "sum_pairs launch"));
   return RECAP_OK;
 }
 

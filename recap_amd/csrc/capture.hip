@@ -8,6 +8,8 @@
 // (drift weight included) and accumulates sum (old - of)^2 and sum of^2.  The reference
 // adds them with float atomics; here each workgroup writes a partial pair and sum_pairs
 // adds them in a fixed order.  Elementwise, HBM-bound, 16-byte accesses.
+#include <mutex>
+
 #include "kernels.hpp"
 
 namespace recap {
@@ -109,6 +111,37 @@ hipError_t run_capture(const CaptureArgs& a, int dtype, int dim, int* blocks_per
   if (dtype == BF16::code)
     return dim == 128 ? launch_capture<BF16, 128>(a, blocks_per_bank, s) : launch_capture<BF16, 64>(a, blocks_per_bank, s);
   return dim == 128 ? launch_capture<F16, 128>(a, blocks_per_bank, s) : launch_capture<F16, 64>(a, blocks_per_bank, s);
+}
+
+// ---------------------------------------------------------------------------------------
+// Static scratch of the allocation-free capture (recap_refresh_capture_noalloc): the
+// per-workgroup validation pairs live in this file-scope device array instead of a caller
+// workspace.  Each GPU holds its own copy until the process ends; its address on a device
+// is looked up once, with that device current, and kept per device.  In host code the
+// array's name is only a host-side stand-in, so kernels and copies get the looked-up
+// address, never the name.
+__device__ __align__(256) float capture_scratch[2 * kCaptureScratchPairs];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_lock;
+float* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+hipError_t capture_scratch_pointer(float** out) {
+  int device = -1;
+  hipError_t e = hipGetDevice(&device);
+  if (e != hipSuccess) return e;
+  if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> guard(g_scratch_lock);
+  if (g_scratch_ptr[device] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(capture_scratch));
+    if (e != hipSuccess) return e;
+    g_scratch_ptr[device] = static_cast<float*>(ptr);
+  }
+  *out = g_scratch_ptr[device];
+  return hipSuccess;
 }
 
 // out2 = fixed-order sums of n (a, b) pairs.

@@ -129,6 +129,10 @@ struct CaptureArgs {
 hipError_t run_capture(const CaptureArgs& a, int dtype, int dim, int* blocks_per_bank,
                        hipStream_t s);
 hipError_t run_sum_pairs(const float* part, int n, float* out2, hipStream_t s);
+// Partial pairs of the allocation-free capture's static scratch (4 MiB per GPU), and its
+// device address on the current device (looked up on the first call per device).
+constexpr int64_t kCaptureScratchPairs = int64_t(1) << 19;
+hipError_t capture_scratch_pointer(float** out);
 hipError_t run_drift_center(const float* part, int banks, int tiles, int rows, float* center,
                             hipStream_t s);
 

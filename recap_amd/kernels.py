@@ -435,6 +435,25 @@ def refresh_capture(dense_out: torch.Tensor, dense_lse: torch.Tensor, head_out: 
     return stats
 
 
+def refresh_capture_noalloc(dense_out: torch.Tensor, dense_lse: torch.Tensor,
+                            head_out: torch.Tensor, head_lse: torch.Tensor, go: torch.Tensor,
+                            gl: torch.Tensor, rowmap: torch.Tensor, geo: Geometry,
+                            det: torch.Tensor, dl: torch.Tensor, stats: torch.Tensor | None,
+                            glref: torch.Tensor | None = None,
+                            center: torch.Tensor | None = None) -> None:
+    """refresh_capture through recap_refresh_capture_noalloc: the library allocates nothing
+    (its validation partials live in a static 4 MiB device array); the caller passes the
+    validation pair's output ``stats`` ([2] fp32) when validating."""
+    b, h, n, d = dense_out.shape
+    if not all(t.is_contiguous() for t in (dense_lse, head_out, head_lse, go, gl, det, dl)):
+        raise ValueError("capture inputs must be contiguous")
+    call("recap_refresh_capture_noalloc", dense_out.data_ptr(), dtype_code(dense_out.dtype), b,
+         h, d, dense_out.stride(0), dense_out.stride(1), dense_out.stride(2),
+         dense_lse.data_ptr(), head_out.data_ptr(), head_lse.data_ptr(), go.data_ptr(),
+         gl.data_ptr(), rowmap.data_ptr(), n, geo.n_video, det.data_ptr(), dl.data_ptr(),
+         _p(glref), _p(center), _p(stats), _stream())
+
+
 def bank_copy_async(dst: torch.Tensor, src: torch.Tensor, stream=None) -> None:
     """Asynchronous device <-> pinned-host copy of a whole bank tensor on ``stream``."""
     if dst.numel() * dst.element_size() != src.numel() * src.element_size():

@@ -242,3 +242,42 @@ def assert_sparse_parity(got, ref, op, q, k, v, wl, device, what, dtype=torch.bf
           f"{int(flip.sum())}); neither {int((~passed).sum())}", flush=True)
     assert bool(passed.all()), f"{what}: {int((~passed).sum())} elements outside the bar"
     assert_parity(got, want, what, dtype=dtype, mask=ok, cos=cos)
+
+
+def capture_inputs(d, dtype, text_first, seed, banks=3, blocks=5):
+    """Synthetic capture inputs covering the capture's cases: ratios spread over (0, 1),
+    ratios above 1 - 1e-3 (zeroed rows), lh >= lf (ratio clamped at 1 - 1e-6), log-mass
+    refinements past +-30 (clamped), on 3 banks of a ragged video (5 blocks + 37 tokens)
+    with 100 text tokens before or after it (``banks`` and ``blocks`` change the size)."""
+    g = torch.Generator().manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    n_video, text = blocks * 128 + 37, 100
+    n = n_video + text
+    rows = (n_video // 128) * 128
+    perm = rng.permutation(n_video)
+    offset = text if text_first else 0
+    text_idx = np.arange(text) if text_first else np.arange(n_video, n)
+    rowmap = np.concatenate([offset + perm, text_idx]).astype(np.int32)
+    of = (1.5 * torch.randn(1, banks, n, d, generator=g)).to(dtype)
+    lf = 2.0 * torch.randn(banks, n, generator=g) + 5.0
+    lf_row = lf[:, torch.as_tensor(rowmap, dtype=torch.long)]           # reordered rows
+    u = torch.rand(banks, n, generator=g) * 0.98 + 0.01
+    kind = torch.randint(0, 10, (banks, n), generator=g)
+    u = torch.where(kind == 0, 1.0 - 1e-4 * torch.rand(banks, n, generator=g), u)  # zeroed
+    u = torch.where(kind == 1, torch.ones(()), u)                       # ratio 1 -> clamp
+    u = torch.where(kind == 2, 1.0 + torch.rand(banks, n, generator=g), u)  # lh > lf
+    lh = (lf_row + torch.log(u)).float()
+    oh = (of[0][:, torch.as_tensor(rowmap, dtype=torch.long)]
+          + 0.3 * torch.randn(banks, n, d, generator=g)).to(dtype)
+    go = torch.randn(banks, rows, d, generator=g).to(dtype)
+    gl = (lf_row[:, :rows] + torch.log1p(-u[:, :rows].clamp_max(0.999))
+          + 0.2 * torch.randn(banks, rows, generator=g)).float()
+    gl[:, ::97] += 45.0     # DL below -30
+    gl[:, 5::89] -= 45.0    # DL above +30
+    old_det = (0.5 * torch.randn(banks, rows, d, generator=g)).to(torch.float16)
+    old_dl = 0.3 * torch.randn(banks, rows, generator=g)
+    glref = gl + 0.1 * torch.randn(banks, rows, generator=g)
+    center = 0.05 * torch.randn(banks, generator=g)
+    return dict(of=of, lf=lf.reshape(1, banks, n), oh=oh, lh=lh, go=go, gl=gl, perm=perm,
+                offset=offset, rowmap=rowmap, n=n, n_video=n_video, rows=rows,
+                old=(old_det, old_dl, glref, center))

@@ -4,57 +4,17 @@ the ten-step paged schedule at the HunyuanVideo-720p shape."""
 
 import math
 
-import numpy as np
 import pytest
 import torch
 
 import oracle as O
-from gpu_util import SMALL, assert_parity, assert_sparse_parity, ulp
+from gpu_util import SMALL, assert_parity, assert_sparse_parity, capture_inputs, ulp
 from recap_amd import HostBankOperator, Operator, OperatorConfig, REFRESH, SPARSE
 from recap_amd import kernels as K
 from recap_amd.layout import Layout, SparseGeometry, hilbert_permutation
 from recap_amd.synthetic import WORKLOADS, make_qkv, perturb
 
 pytestmark = pytest.mark.gpu
-
-
-def _capture_inputs(d, dtype, text_first, seed):
-    """Synthetic capture inputs covering the capture's cases: ratios spread over (0, 1),
-    ratios above 1 - 1e-3 (zeroed rows), lh >= lf (ratio clamped at 1 - 1e-6), log-mass
-    refinements past +-30 (clamped), on 3 banks of a ragged video (5 blocks + 37 tokens)
-    with 100 text tokens before or after it."""
-    g = torch.Generator().manual_seed(seed)
-    rng = np.random.default_rng(seed)
-    banks, n_video, text = 3, 5 * 128 + 37, 100
-    n = n_video + text
-    rows = (n_video // 128) * 128
-    perm = rng.permutation(n_video)
-    offset = text if text_first else 0
-    text_idx = np.arange(text) if text_first else np.arange(n_video, n)
-    rowmap = np.concatenate([offset + perm, text_idx]).astype(np.int32)
-    of = (1.5 * torch.randn(1, banks, n, d, generator=g)).to(dtype)
-    lf = 2.0 * torch.randn(banks, n, generator=g) + 5.0
-    lf_row = lf[:, torch.as_tensor(rowmap, dtype=torch.long)]           # reordered rows
-    u = torch.rand(banks, n, generator=g) * 0.98 + 0.01
-    kind = torch.randint(0, 10, (banks, n), generator=g)
-    u = torch.where(kind == 0, 1.0 - 1e-4 * torch.rand(banks, n, generator=g), u)  # zeroed
-    u = torch.where(kind == 1, torch.ones(()), u)                       # ratio 1 -> clamp
-    u = torch.where(kind == 2, 1.0 + torch.rand(banks, n, generator=g), u)  # lh > lf
-    lh = (lf_row + torch.log(u)).float()
-    oh = (of[0][:, torch.as_tensor(rowmap, dtype=torch.long)]
-          + 0.3 * torch.randn(banks, n, d, generator=g)).to(dtype)
-    go = torch.randn(banks, rows, d, generator=g).to(dtype)
-    gl = (lf_row[:, :rows] + torch.log1p(-u[:, :rows].clamp_max(0.999))
-          + 0.2 * torch.randn(banks, rows, generator=g)).float()
-    gl[:, ::97] += 45.0     # DL below -30
-    gl[:, 5::89] -= 45.0    # DL above +30
-    old_det = (0.5 * torch.randn(banks, rows, d, generator=g)).to(torch.float16)
-    old_dl = 0.3 * torch.randn(banks, rows, generator=g)
-    glref = gl + 0.1 * torch.randn(banks, rows, generator=g)
-    center = 0.05 * torch.randn(banks, generator=g)
-    return dict(of=of, lf=lf.reshape(1, banks, n), oh=oh, lh=lh, go=go, gl=gl, perm=perm,
-                offset=offset, rowmap=rowmap, n=n, n_video=n_video, rows=rows,
-                old=(old_det, old_dl, glref, center))
 
 
 @pytest.mark.parametrize("d,dtype,text_first,validate", [
@@ -66,7 +26,7 @@ def test_refresh_capture_vs_oracle_identical_inputs(cuda, d, dtype, text_first, 
     head branch, coarse tail, and for validation the old refinement with its drift inputs):
     D within its fp16 rounding plus the conditioning of (of - ratio oh) / (1 - ratio), DL
     within fp32 rounding, identical zeroed rows, validation sums within 1e-4 relative."""
-    x = _capture_inputs(d, dtype, text_first, seed=d + 7 * int(validate))
+    x = capture_inputs(d, dtype, text_first, seed=d + 7 * int(validate))
     print(f"case d={d} {dtype} text_first={text_first} validate={validate}", flush=True)
     banks, rows = x["oh"].shape[0], x["rows"]
     det = x["old"][0].clone() if validate else torch.zeros(banks, rows, d, dtype=torch.float16)

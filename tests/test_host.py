@@ -34,6 +34,18 @@ def test_library_exports_every_declared_symbol():
     assert lib.recap_abi_version() == _lib.ABI_VERSION
 
 
+def test_noalloc_capture_size_limit_is_checked_on_the_host():
+    """recap_refresh_capture_noalloc rejects a validation whose partial pairs exceed its
+    static scratch before it touches a device (the pointers here are never dereferenced)."""
+    d, n_video = 128, 128 * 64
+    per_bank = int(_lib.load().recap_capture_partials(1, d, n_video))
+    banks = _lib.CAPTURE_NOALLOC_MAX_PAIRS // per_bank + 1
+    with pytest.raises(ValueError, match="static scratch holds"):
+        _lib.call("recap_refresh_capture_noalloc", 16, _lib.RECAP_BF16, 1, banks, d,
+                  banks * n_video * d, n_video * d, d, 16, 16, 16, 16, 16, 16, n_video,
+                  n_video, 16, 16, 16, 16, 16, None)
+
+
 @pytest.mark.parametrize("name", list(WORKLOADS))
 def test_native_hilbert_matches_oracle(name):
     grid = WORKLOADS[name].grid
