@@ -1,13 +1,16 @@
 #!/usr/bin/env python3
 """Benchmark of the corrected sparse-attention call on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--workload hunyuan-720p]
+    python bench.py [--steps K] [--warmup W] [--workload hunyuan-720p] [--no-sequence]
 
 One "step" is one corrected SPARSE call (Operator.attend after a REFRESH) at the
 HunyuanVideo-720p shape: B=1, 24 heads x 128, 118,800 video + 256 text tokens, 128-token
 blocks, 20% density, bf16, inputs resident in HBM and drifted 2% from the refresh inputs.
 The timed region is K calls bracketed by torch.cuda.synchronize(); per-stage durations come
-from HIP events recorded on the same stream inside the timed calls.  Prints one JSON line.
+from HIP events recorded on the same stream inside the timed calls.  The default run then adds
+the ten-step schedule with refinement banks paged through pinned host memory (20 layers,
+REFRESH at steps 0 and 5; ms_per_step_host_banks, copy_overlap_fraction).  Prints one JSON
+line.
 """
 
 from __future__ import annotations
@@ -123,12 +126,14 @@ def step_sequence(wl, layers: int, steps: int, refresh_at: tuple, drift: float) 
     layout = Layout.from_permutation(hilbert_permutation(wl.grid), text_tokens=wl.text_tokens,
                                      text_first=wl.text_first)
     geometry = SparseGeometry.build(layout, 128)
-    base = make_qkv(wl, seed=0, device=dev)
-    inputs = []
-    for step in range(steps):
-        base = tuple(perturb(x, drift, seed=i, step=step + 1) for i, x in enumerate(base))
-        inputs.append(base)
-        torch.cuda.synchronize()
+
+    def step_inputs():
+        """The drifting inputs step by step (each step's from the previous one); generated
+        outside the timed region of its step, and identical for both runs."""
+        x = make_qkv(wl, seed=0, device=dev)
+        for step in range(steps):
+            x = tuple(perturb(t, drift, seed=i, step=step + 1) for i, t in enumerate(x))
+            yield x
 
     def run(cls, host: bool):
         cfg = OperatorConfig(head_density=wl.density, host_banks=host)
@@ -137,9 +142,8 @@ def step_sequence(wl, layers: int, steps: int, refresh_at: tuple, drift: float) 
             op.preallocate_host(layers, wl.heads, wl.dim)
             op.record_copies = True
         times, outs = [], None
-        for step in range(steps):
+        for step, (q, k, v) in enumerate(step_inputs()):
             kind = REFRESH if step in refresh_at else SPARSE
-            q, k, v = inputs[step]
             torch.cuda.synchronize()
             start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             start.record()
@@ -161,7 +165,7 @@ def step_sequence(wl, layers: int, steps: int, refresh_at: tuple, drift: float) 
             op.finish()
         del op
         torch.cuda.empty_cache()
-        return times, copy_ms, host_bytes, outs
+        return times, copy_ms, host_bytes, outs.clone()
 
     t_host, copy_ms, host_bytes, out_host = run(HostBankOperator, True)
     t_gpu, _, _, out_gpu = run(Operator, False)
@@ -252,6 +256,8 @@ def main() -> int:
                     help="run only the step sequence with paged banks (20 layers, 10 steps, "
                          "REFRESH at 0 and 5, 3%% drift) and print its JSON line")
     ap.add_argument("--layers", type=int, default=20, help="layers of the step sequence")
+    ap.add_argument("--no-sequence", action="store_true",
+                    help="skip the paged step sequence of the default run")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: --gpus {args.gpus} is not supported in this build "
@@ -396,6 +402,18 @@ def main() -> int:
             result["cpu_baseline"] = cpu_baseline(op, q1, k1, v1, wl, args.cpu_heads)
             log(f"[bench] CPU baseline {result['cpu_baseline']['value']} ms/call "
                 f"({result['cpu_baseline']['sample']})")
+        if not args.no_sequence:
+            # The ten-step schedule with paged refinement banks: REFRESH at steps 0 and 5,
+            # SPARSE otherwise, 3% drift, args.layers layers; paged vs resident banks.
+            del op, q0, k0, v0, kv
+            torch.cuda.empty_cache()
+            seq = step_sequence(wl, args.layers, 10, (0, 5), 0.03)
+            result["ms_per_step_host_banks"] = seq["ms_per_step_host_banks"]
+            result["copy_overlap_fraction"] = seq["copy_overlap_fraction"]
+            result["sequence"] = seq
+            log(f"[bench] sequence: {seq['ms_per_step_host_banks']} ms/step paged, "
+                f"{seq['ms_per_step_gpu_banks']} resident, copy overlap "
+                f"{seq['copy_overlap_fraction']}")
     print(json.dumps(result), flush=True)
     return 0
 

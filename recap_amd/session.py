@@ -1,19 +1,21 @@
 """The per-sample step loop around a transformer's ``forward`` (recap/session.py).
 
-Each denoising step takes one decision, shared by the ``calls_per_step`` transformer calls
-a pipeline makes per step (one per guidance branch):
+Every denoising step gets one decision, shared by the ``calls_per_step`` transformer calls a
+pipeline makes per step (one per guidance branch):
 
 ``EXACT``    dense evaluation;
 ``REFRESH``  dense evaluation that also renews every layer's attention refinement and
              scores the old one;
 ``SPARSE``   corrected sparse evaluation (the operator's hot path);
-``REUSE``    no evaluation: the output is extrapolated from the prediction cache as
-             ``o + g h v`` (latest computed output ``o``, its velocity ``v`` per step,
-             ``h`` steps ahead), with the gain ``g`` fitted online by least squares over
-             every computed step.
+``REUSE``    no evaluation: each stream's output is extrapolated as ``o + g h v`` from its
+             latest computed output ``o`` and velocity ``v`` (per step), ``h`` steps ahead,
+             with one gain ``g`` fitted by least squares over the computed steps.
 
-The prediction cache and all the arithmetic on it stay on the device of the outputs; the
-only host values are the scalar norms the controller needs.
+The pieces: ``_Planner`` decides a step from the controller (recap_amd/controller.py) and
+the sample's progress; ``_StreamCache`` holds one stream's prediction state on the device of
+its outputs; ``_GainFit`` is the running least-squares gain; ``RecapSession`` wraps the
+forward, runs the operator and keeps the per-step records (keys ``t, a, h, m, g, sec,
+validation``, the reference's record format).
 """
 
 from __future__ import annotations
@@ -21,6 +23,7 @@ from __future__ import annotations
 import dataclasses
 import math
 import time
+from dataclasses import dataclass, field
 from typing import Any
 
 import torch
@@ -30,28 +33,190 @@ from .controller import Controller
 from .operator import EXACT, REFRESH, SPARSE, Operator
 
 REUSE = "reuse"
-_COMPUTE = "compute"   # cover decision: evaluate (dense or refresh)
-_SPARSE_COVER = "sparse"
 
 
-def _sample_of(out: Any) -> torch.Tensor:
-    """The prediction tensor of a transformer output (tensor, tuple or ``.sample``)."""
+# -- transformer outputs ------------------------------------------------------------------
+
+
+def _prediction(out: Any) -> torch.Tensor:
+    """The prediction tensor of a transformer output: a tensor, a tuple's first item or a
+    ``.sample`` field."""
     if isinstance(out, tuple):
         return out[0]
-    return out.sample if hasattr(out, "sample") else out
+    return getattr(out, "sample", out)
 
 
-def _with_sample(template: Any, tensor: torch.Tensor) -> Any:
-    """``template`` with its prediction replaced by ``tensor``."""
+def _replace_prediction(template: Any, tensor: torch.Tensor) -> Any:
+    """``template`` with its prediction tensor replaced."""
     if isinstance(template, tuple):
-        return (tensor,) + tuple(template[1:])
+        return (tensor, *template[1:])
     if hasattr(template, "sample"):
         return dataclasses.replace(template, sample=tensor)
     return tensor
 
 
+# -- prediction state ---------------------------------------------------------------------
+
+
+@dataclass
+class _GainFit:
+    """g = sum <delta, h v> / sum |h v|^2 over computed steps; a step's terms are staged
+    while its streams run and enter the fit when the step completes."""
+
+    value: float = 0.0
+    num: float = 0.0
+    den: float = 0.0
+    staged_num: float = 0.0
+    staged_den: float = 0.0
+
+    def stage(self, num: float, den: float) -> None:
+        self.staged_num += num
+        self.staged_den += den
+
+    def commit(self) -> None:
+        if self.staged_den > 0.0:
+            self.num += self.staged_num
+            self.den += self.staged_den
+            self.value = self.num / max(self.den, 1e-30)
+        self.staged_num = self.staged_den = 0.0
+
+
+@dataclass
+class _StreamCache:
+    """One stream's latest computed output (fp32, on its device), its velocity per step,
+    and the output object and dtype an extrapolated step is returned in."""
+
+    output: torch.Tensor
+    template: Any
+    dtype: torch.dtype
+    velocity: torch.Tensor | None = None
+
+    @torch.no_grad()
+    def absorb(self, output: torch.Tensor, template: Any, dtype: torch.dtype, h: int,
+               gain: float, fit: _GainFit) -> tuple[torch.Tensor, torch.Tensor]:
+        """Take the output computed ``h`` steps after the cached one.  Returns the squared
+        norms of the extrapolation's miss (``o + g h v`` against the new output, or the step
+        itself before a velocity exists) and of the new output, and stages the gain's
+        terms."""
+        change = output - self.output
+        miss = change
+        if self.velocity is not None:
+            predicted = self.velocity * float(h)
+            if gain:
+                miss = change - predicted * gain
+            norm_sq = float(torch.linalg.vector_norm(predicted) ** 2)
+            if norm_sq > 0.0:
+                fit.stage(float((change * predicted).sum()), norm_sq)
+        self.output, self.velocity = output, change / float(h)
+        self.template, self.dtype = template, dtype
+        return torch.linalg.vector_norm(miss) ** 2, torch.linalg.vector_norm(output) ** 2
+
+    @torch.no_grad()
+    def extrapolate(self, h: int, gain: float) -> Any:
+        if not gain or self.velocity is None:
+            return self.template
+        guess = (self.output + self.velocity * (gain * float(h))).to(self.dtype)
+        return _replace_prediction(self.template, guess)
+
+
+# -- decisions ----------------------------------------------------------------------------
+
+
+@dataclass
+class _Progress:
+    """Where the sample stands: the last computed and refreshed steps, whether the
+    refinement phase has begun, and the midpoint check after the last refresh (the first
+    step half-way to the end, which is validated when it runs sparse)."""
+
+    last_computed: int | None = None
+    last_refresh: int | None = None
+    refining: bool = False
+    midpoint: int | None = None
+    midpoint_checked: bool = False
+
+
+class _Planner:
+    """The decision of one step (recap/session.py:109-172).
+
+    First whether the step is covered by extrapolation (``REUSE``) or computed, and whether
+    a computed step may run sparse; then the kind: ``EXACT`` before the refinement phase and
+    in the exact tail, ``SPARSE`` inside a valid refinement lease, ``REFRESH`` otherwise.
+    """
+
+    DENSE, SPARSE_OK = "dense", "sparse-ok"
+
+    def __init__(self, config: RecapConfig, controller: Controller, operator: Operator,
+                 progress: _Progress):
+        self.schedule = config.schedule
+        self.ctl, self.op, self.prog = controller, operator, progress
+
+    def _cover(self, t: int) -> str:
+        ctl, prog, schedule = self.ctl, self.prog, self.schedule
+        if prog.last_computed is None:
+            return self.DENSE                       # nothing to extrapolate from yet
+        if ctl.in_exact_tail(t):
+            return REUSE if ctl.budget_spent() else self.DENSE
+        if ctl.budget_spent_before_tail():
+            return REUSE                            # what is left is the tail's
+        if not ctl.licensed:
+            early = t < schedule.prefix_floor
+            due = ctl.half_budget_spent() or (schedule.prefix_cap and t >= schedule.prefix_cap)
+            if early or not due:
+                return self.DENSE
+            ctl.start_reuse()                       # the prefix ran out: reuse from now on
+        if t - prog.last_computed < ctl.reuse_span(t):
+            return REUSE
+        fresh = (self.op.banks_valid and prog.refining and prog.last_refresh is not None
+                 and ctl.refinement_usable(t - prog.last_refresh))
+        return self.SPARSE_OK if fresh else self.DENSE
+
+    def _final_step_sparse(self, t: int) -> bool:
+        """The last step runs sparse when the span from the midpoint check to it is longer
+        than what that check validated (or there was no check), the refinement is usable
+        and budget remains."""
+        prog = self.prog
+        if t != self.schedule.num_steps - 1 or not self.op.banks_valid:
+            return False
+        if prog.last_refresh is not None and prog.midpoint is not None and prog.midpoint_checked:
+            validated = prog.midpoint - (prog.last_refresh + 1)
+            if t - prog.midpoint <= validated:
+                return False
+        if prog.last_refresh is not None and not self.ctl.refinement_usable(t - prog.last_refresh):
+            return False
+        return not self.ctl.budget_spent()
+
+    def decide(self, t: int) -> str:
+        cover = self._cover(t)
+        if cover != REUSE and self.ctl.in_exact_tail(t):
+            return EXACT
+        if self._final_step_sparse(t):
+            cover = self.SPARSE_OK
+        if cover == REUSE:
+            return REUSE
+        if cover == self.DENSE and self.ctl.licensed:
+            self.prog.refining = True               # the first computation once reuse began
+        if not self.prog.refining:
+            return EXACT
+        return SPARSE if cover == self.SPARSE_OK and self.op.banks_valid else REFRESH
+
+
+# -- the session --------------------------------------------------------------------------
+
+
+@dataclass
+class _StepLog:
+    """The running step's decision and measurements across its streams."""
+
+    action: str | None = None
+    gain: float = 0.0
+    seconds: float = 0.0
+    miss_sq: list = field(default_factory=list)
+    output_sq: list = field(default_factory=list)
+
+
 class RecapSession:
-    """Per-sample scheduling state wrapped around a transformer (recap/session.py:44-359)."""
+    """Per-sample scheduling state wrapped around a transformer (recap/session.py:46-359).
+    Call :meth:`reset` before every sample."""
 
     def __init__(self, config: RecapConfig, operator: Operator, *, calls_per_step: int = 1,
                  model_info: dict[str, Any] | None = None):
@@ -61,207 +226,83 @@ class RecapSession:
         if self.calls_per_step < 1:
             raise ValueError("calls_per_step must be positive")
         if operator.n_streams != self.calls_per_step:
-            raise ValueError(
-                f"operator has {operator.n_streams} streams but the pipeline makes "
-                f"{self.calls_per_step} transformer calls per step")
+            raise ValueError(f"operator has {operator.n_streams} streams but the pipeline makes "
+                             f"{self.calls_per_step} transformer calls per step")
         self.model_info = dict(model_info or {})
         self._transformer = None
         self._wrapped_forward = None
         self.reset()
 
-    # -- per-sample state ------------------------------------------------------------------
-
     def reset(self) -> None:
-        """Start a new sample (call before every pipeline call)."""
-        transformer = self._transformer
-        if transformer is not None and transformer.forward is not self._wrapped_forward:
-            # Offload hooks may have restored the unwrapped forward.
-            self._wrap(transformer)
+        """Start a new sample."""
+        tr = self._transformer
+        if tr is not None and tr.forward is not self._wrapped_forward:
+            self._wrap(tr)      # offload hooks restored the unwrapped forward
         self.controller = Controller(self.config.schedule)
         self.operator.reset()
+        self.progress = _Progress()
+        self.planner = _Planner(self.config, self.controller, self.operator, self.progress)
+        self.caches: list[_StreamCache | None] = [None] * self.calls_per_step
+        self.fit = _GainFit()
+        self.log = _StepLog()
+        self.actions: list[dict] = []
         self.step = 0
         self.call_index = 0
-        self.last_computed: int | None = None
-        self.last_refresh: int | None = None
-        self.phase_active = False
-        self.actions: list[dict] = []
-        n = self.calls_per_step
-        self.caches: list[dict | None] = [None] * n   # per stream: {"o": ..., "v": ...}
-        self.output_objects: list[Any] = [None] * n
-        self.output_dtypes: list[torch.dtype | None] = [None] * n
-        self.gain = 0.0
-        self._gain_num = 0.0
-        self._gain_den = 0.0
-        self.midpoint_step: int | None = None
-        self.midpoint_done = False
-        self._begin_step_state(None)
 
-    def _begin_step_state(self, action: str | None) -> None:
-        self._step_action = action
-        self._step_gain = self.gain
-        self._step_seconds = 0.0
-        self._step_residual_sq: list[torch.Tensor] = []
-        self._step_output_sq: list[torch.Tensor] = []
-        self._step_gain_num = 0.0
-        self._step_gain_den = 0.0
+    @property
+    def gain(self) -> float:
+        return self.fit.value
 
-    # -- decisions -------------------------------------------------------------------------
-
-    def _cover(self, t: int) -> str:
-        """Whether step t is computed, reused or (if allowed) sparse."""
-        ctl = self.controller
-        if self.last_computed is None:
-            return _COMPUTE
-        if ctl.in_exact_tail(t):
-            return REUSE if ctl.budget_exhausted() else _COMPUTE
-        if ctl.mid_budget_exhausted():
-            return REUSE
-        if not ctl.licensed:
-            schedule = self.config.schedule
-            if t < schedule.prefix_floor:
-                return _COMPUTE
-            if ctl.prefix_overspent() or (schedule.prefix_cap and t >= schedule.prefix_cap):
-                ctl.license()
-            else:
-                return _COMPUTE
-        if t - self.last_computed < ctl.allowed_gap(t):
-            return REUSE
-        if not self.phase_active or not self.operator.banks_valid:
-            return _COMPUTE
-        if self.last_refresh is None or not ctl.lease_ok(t - self.last_refresh):
-            return _COMPUTE  # the refinement is too old: refresh it
-        return _SPARSE_COVER
-
-    def _terminal_unvalidated(self, t: int) -> bool:
-        """Is step t farther from the midpoint check than the span that check validated?"""
-        if self.last_refresh is None or self.midpoint_step is None or not self.midpoint_done:
-            return True
-        validated = self.midpoint_step - (self.last_refresh + 1)
-        return t - self.midpoint_step > validated
-
-    def _terminal_sparse(self, t: int) -> bool:
-        """Compute the final step sparsely when its interval is not validated."""
-        schedule = self.config.schedule
-        if not (t == schedule.num_steps - 1 and self.operator.banks_valid
-                and self._terminal_unvalidated(t)):
-            return False
-        if self.last_refresh is not None and not self.controller.lease_ok(t - self.last_refresh):
-            return False
-        return not self.controller.budget_exhausted()
-
-    def _action(self, t: int) -> str:
-        cover = self._cover(t)
-        if cover != REUSE and self.controller.in_exact_tail(t):
-            return EXACT
-        if self._terminal_sparse(t):
-            cover = _SPARSE_COVER
-        if cover == REUSE:
-            return REUSE
-        if cover == _COMPUTE and self.controller.licensed and not self.phase_active:
-            self.phase_active = True  # the first computation once reuse has started
-        if not self.phase_active:
-            return EXACT
-        if cover == _SPARSE_COVER and self.operator.banks_valid:
-            return SPARSE
-        return REFRESH
+    # -- one step ------------------------------------------------------------------------
 
     def begin(self, t: int) -> str:
-        """Decide step t and prepare the operator for it."""
-        action = self._action(t)
+        """Decide step t; a computed step counts against the budget and sets the operator's
+        kind (recap/session.py:231-238)."""
+        action = self.planner.decide(t)
         if action != REUSE:
-            self.controller.computed += 1
+            self.controller.count_computed()
             self.operator.begin_step(t, action)
-            if t == self.midpoint_step and action == SPARSE:
-                self.midpoint_done = True
+            if action == SPARSE and t == self.progress.midpoint:
+                self.progress.midpoint_checked = True
         return action
 
-    def complete(self, t: int, action: str, diagnostics: dict[str, Any]) -> dict[str, Any]:
-        """Record a computed step and feed its measurements to the controller."""
-        row: dict[str, Any] = {"t": t, "a": action}
-        if action == REFRESH:
-            row.update(self._after_refresh(t))
-        row.update(diagnostics)
-        if "m" in row and "h" in row:
-            self.controller.observe_residual(int(row["h"]), float(row["m"]), t)
-        self.last_computed = t
-        return row
-
     def _after_refresh(self, t: int) -> dict[str, Any]:
+        """Score the refinement just replaced and set the next midpoint check."""
         out: dict[str, Any] = {}
-        measured = self.operator.drain_validation()
-        if measured is not None:
-            age, error = measured
-            passed = self.controller.observe_validation(age, error)
-            record = {"t": t, "age": age, "error": round(error, 6), "passed": passed}
-            self.controller.validations.append(record)
-            out["validation"] = record
-        self.last_refresh = t
+        scored = self.operator.drain_validation()
+        if scored is not None:
+            age, error = scored
+            passed = self.controller.record_refinement_error(age, error)
+            out["validation"] = {"t": t, "age": age, "error": round(error, 6), "passed": passed}
+            self.controller.validations.append(out["validation"])
         last = self.config.schedule.num_steps - 1
-        self.midpoint_step = int(math.ceil((t + last) / 2.0))
-        self.midpoint_done = False
+        self.progress.last_refresh = t
+        self.progress.midpoint = int(math.ceil((t + last) / 2.0))
+        self.progress.midpoint_checked = False
         return out
 
-    # -- prediction cache ------------------------------------------------------------------
+    def _close_step(self, t: int) -> dict[str, Any]:
+        """The computed step's record: the relative miss ``m`` of the extrapolation over all
+        streams and the gain after this step."""
+        log = self.log
+        row: dict[str, Any] = {"t": t, "a": log.action}
+        if log.action == REFRESH:
+            row.update(self._after_refresh(t))
+        self.fit.commit()
+        if log.miss_sq:
+            miss = torch.sqrt(torch.stack(log.miss_sq).sum())
+            size = torch.sqrt(torch.stack(log.output_sq).sum())
+            h = t - int(self.progress.last_computed)
+            row.update(h=h, m=round(float(miss / size.clamp_min(1e-30)), 6),
+                       g=round(self.fit.value, 4))
+            self.controller.record_mismatch(h, row["m"], t)
+        self.progress.last_computed = t
+        return row
 
-    @torch.no_grad()
-    def _observe_stream(self, t: int, stream: int, output: torch.Tensor) -> None:
-        """Renew stream's prediction cache with a computed output; accumulate the
-        mismatch of what the extrapolation would have given and the gain's normal
-        equation (sums of <delta, h v> and |h v|^2)."""
-        cache = self.caches[stream]
-        if cache is None:
-            self.caches[stream] = {"o": output, "v": None}
-            return
-        if self.last_computed is None:
-            raise RuntimeError("prediction cache exists without a previous computed step")
-        h = t - int(self.last_computed)
-        if h <= 0:
-            raise RuntimeError(f"non-positive computed-state gap {h} at step {t}")
-        delta = output - cache["o"]
-        velocity = cache["v"]
-        residual = delta
-        if velocity is not None:
-            predicted = velocity * float(h)
-            if self._step_gain:
-                residual = delta - predicted * self._step_gain
-            pred_sq = float(torch.linalg.vector_norm(predicted) ** 2)
-            if pred_sq > 0.0:
-                self._step_gain_num += float((delta * predicted).sum())
-                self._step_gain_den += pred_sq
-        self._step_residual_sq.append(torch.linalg.vector_norm(residual) ** 2)
-        self._step_output_sq.append(torch.linalg.vector_norm(output) ** 2)
-        self.caches[stream] = {"o": output, "v": delta / float(h)}
-
-    def _finish_observation(self, t: int) -> dict[str, Any]:
-        """The step's relative mismatch over all streams and the updated gain."""
-        if not self._step_residual_sq:
-            return {}
-        if self._step_gain_den > 0.0:
-            self._gain_num += self._step_gain_num
-            self._gain_den += self._step_gain_den
-            self.gain = self._gain_num / max(self._gain_den, 1e-30)
-        residual = torch.sqrt(torch.stack(self._step_residual_sq).sum())
-        output = torch.sqrt(torch.stack(self._step_output_sq).sum())
-        misfit = float(residual / output.clamp_min(1e-30))
-        h = t - int(self.last_computed)
-        return {"h": h, "m": round(misfit, 6), "g": round(self.gain, 4)}
-
-    def _reuse(self, t: int, stream: int) -> Any:
-        cache = self.caches[stream]
-        if cache is None or self.last_computed is None:
-            raise RuntimeError("reuse requested before any computed step")
-        velocity = cache["v"]
-        if self.gain and velocity is not None:
-            h = t - int(self.last_computed)
-            extrapolated = (cache["o"] + velocity * (self.gain * float(h))).to(
-                self.output_dtypes[stream])
-            return _with_sample(self.output_objects[stream], extrapolated)
-        return self.output_objects[stream]
-
-    # -- the wrapped forward ---------------------------------------------------------------
+    # -- the wrapped forward -------------------------------------------------------------
 
     def install(self, transformer) -> None:
-        """Wrap ``transformer.forward`` with the step loop."""
+        """Wrap ``transformer.forward`` with the step loop (recap/session.py:252-316)."""
         if getattr(transformer, "_recap_installed", False):
             raise RuntimeError("this transformer already has a RECAP step loop")
         self._transformer = transformer
@@ -278,58 +319,67 @@ class RecapSession:
         self._wrapped_forward = forward
 
     def _call(self, inner, args, kwargs):
-        streams = self.calls_per_step
-        stream, t = self.call_index % streams, self.call_index // streams
-        if t >= self.config.schedule.num_steps:
+        streams, num_steps = self.calls_per_step, self.config.schedule.num_steps
+        t, stream = divmod(self.call_index, streams)
+        if t >= num_steps:
             raise RuntimeError(
                 f"transformer call {self.call_index} is past the configured horizon of "
-                f"{self.config.schedule.num_steps} steps x {streams} calls; check "
-                "schedule.num_steps and the pipeline's guidance settings")
+                f"{num_steps} steps x {streams} calls; check schedule.num_steps and the "
+                "pipeline's guidance settings")
         started = time.perf_counter()
         if stream == 0:
-            self._begin_step_state(self.begin(t))
-        action = self._step_action
-        last_stream = stream == streams - 1
-
-        if action == REUSE:
-            out = self._reuse(t, stream)
-            self._step_seconds += time.perf_counter() - started
-            self.call_index += 1
-            if last_stream:
-                self.actions.append({"t": t, "a": REUSE, "h": t - int(self.last_computed),
-                                     "g": round(self.gain, 4),
-                                     "sec": round(self._step_seconds, 4)})
-                self.step = t + 1
-            return out
-
-        self.operator.set_stream(stream)
-        out = inner(*args, **kwargs)
-        if self.config.sync_step_timing and torch.cuda.is_available():
-            torch.cuda.synchronize()
-        self._step_seconds += time.perf_counter() - started
-        sample = _sample_of(out)
-        self._observe_stream(t, stream, sample.detach().float())
-        self.output_objects[stream] = out
-        self.output_dtypes[stream] = sample.dtype
+            self.log = _StepLog(action=self.begin(t), gain=self.fit.value)
+        log = self.log
+        if log.action == REUSE:
+            cache = self.caches[stream]
+            if cache is None or self.progress.last_computed is None:
+                raise RuntimeError("reuse requested before any computed step")
+            out = cache.extrapolate(t - self.progress.last_computed, self.fit.value)
+        else:
+            self.operator.set_stream(stream)
+            out = inner(*args, **kwargs)
+            if self.config.sync_step_timing and torch.cuda.is_available():
+                torch.cuda.synchronize()
+            self._observe(t, stream, out)
+        log.seconds += time.perf_counter() - started
         self.call_index += 1
-        if last_stream:
-            row = self.complete(t, action, self._finish_observation(t))
-            row["sec"] = round(self._step_seconds, 3)
+        if stream == streams - 1:
+            if log.action == REUSE:
+                row = {"t": t, "a": REUSE, "h": t - int(self.progress.last_computed),
+                       "g": round(self.fit.value, 4), "sec": round(log.seconds, 4)}
+            else:
+                row = self._close_step(t)
+                row["sec"] = round(log.seconds, 3)
             self.actions.append(row)
             self.step = t + 1
         return out
 
-    # -- records ---------------------------------------------------------------------------
+    def _observe(self, t: int, stream: int, out: Any) -> None:
+        """Fold a computed output into its stream's cache; measure the extrapolation's miss
+        from the second computed step on."""
+        prediction = _prediction(out)
+        output = prediction.detach().float()
+        cache = self.caches[stream]
+        if cache is None:
+            self.caches[stream] = _StreamCache(output, out, prediction.dtype)
+            return
+        if self.progress.last_computed is None:
+            raise RuntimeError("prediction cache exists without a previous computed step")
+        h = t - int(self.progress.last_computed)
+        if h <= 0:
+            raise RuntimeError(f"non-positive computed-state gap {h} at step {t}")
+        miss_sq, output_sq = cache.absorb(output, out, prediction.dtype, h, self.log.gain,
+                                          self.fit)
+        self.log.miss_sq.append(miss_sq)
+        self.log.output_sq.append(output_sq)
+
+    # -- records -------------------------------------------------------------------------
 
     def summary(self) -> dict[str, Any]:
         counts: dict[str, int] = {}
         for row in self.actions:
             counts[row["a"]] = counts.get(row["a"], 0) + 1
-        return {
-            "model": dict(self.model_info),
-            "counts": counts,
-            "schedule": [row["a"] for row in self.actions],
-            "per_step_sec": [row.get("sec") for row in self.actions],
-            "reuse_gain_final": round(self.gain, 4),
-            **self.controller.state(),
-        }
+        return {"model": dict(self.model_info), "counts": counts,
+                "schedule": [row["a"] for row in self.actions],
+                "per_step_sec": [row.get("sec") for row in self.actions],
+                "reuse_gain_final": round(self.fit.value, 4), **self.controller.state()}

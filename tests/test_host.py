@@ -211,6 +211,30 @@ def test_config_loader_and_profiles(tmp_path):
             C.OperatorConfig(**{field: value}).validate()
     with pytest.raises(ValueError, match="128"):
         C.GeometryConfig(grid=(1, 2, 3), block_size=64).validate()
+    # the schedule's relations between fields
+    for kw, msg in [({"prefix_floor": 3, "prefix_cap": 2}, "prefix_cap"),
+                    ({"budget": 5, "tail_exact": 5}, "budget"),
+                    ({"num_steps": 3, "tail_exact": 3}, "num_steps"),
+                    ({"budget": 2}, "budget"), ({"tau": 0.0}, "tau")]:
+        with pytest.raises(ValueError, match=msg):
+            C.ScheduleConfig(**kw).validate()
+    C.ScheduleConfig(prefix_floor=3, prefix_cap=0, budget=5, tail_exact=4).validate()
+    # operating points: B an int (not a bool) >= 3, tolerances finite and positive
+    for point in [(True, 0.1, 0.1), (3.0, 0.1, 0.1), (3, float("inf"), 0.1), (3, 0.1, -1.0)]:
+        with pytest.raises(ValueError):
+            C.OperatingPoint(*point).validate()
+    # profile sections: objects only, known keys only, values read per field
+    profile = {"geometry": {"grid": [2, "4", 8], "text_tokens": "16"},
+               "operator": {"head_density": 0.3}, "schedule": {"budget": "7"}}
+    cfg = C.config_from_profile("hunyuan", profile)
+    assert cfg.geometry.grid == (2, 4, 8) and cfg.geometry.text_tokens == 16
+    assert cfg.schedule.budget == 7 and cfg.operator.block_size == 128
+    with pytest.raises(TypeError, match="object"):
+        C.config_from_profile("hunyuan", {**profile, "operator": [1]})
+    with pytest.raises(ValueError, match="unknown key"):
+        C.config_from_profile("hunyuan", {**profile, "operator": {"density": 0.3}})
+    with pytest.raises(ValueError, match="grid"):
+        C.config_from_profile("hunyuan", {"geometry": {"text_tokens": 3}})
 
 
 def test_operator_host_errors():

@@ -87,37 +87,61 @@ def config(**schedule):
 
 def test_controller_license_interval_growth_and_lease():
     ctl = Controller(ScheduleConfig(num_steps=20, tau=0.1))
-    ctl.observe_residual(1, 0.05, t=1)
+    ctl.record_mismatch(1, 0.05, t=1)
     assert not ctl.licensed
-    ctl.observe_residual(1, 0.2, t=2)        # a miss resets the streak
-    ctl.observe_residual(1, 0.05, t=3)
+    ctl.record_mismatch(1, 0.2, t=2)         # a miss resets the run of passes
+    ctl.record_mismatch(1, 0.05, t=3)
     assert not ctl.licensed
-    ctl.observe_residual(1, 0.05, t=4)
-    assert ctl.licensed and ctl.next_gap == 2
-    ctl.observe_residual(2, 0.1, t=6)        # rate 0.05 < tau: interval grows by 2
-    assert ctl.next_gap == 4
-    ctl.observe_residual(4, 0.8, t=10)       # rate 0.2: the interval is kept
-    assert ctl.next_gap == 4
-    assert ctl.observe_validation(age=3, error=0.05)
-    assert ctl.lease_ok(5) and not ctl.lease_ok(6)
-    assert ctl.observe_validation(age=2, error=0.05)   # the lease span grows by 2
-    assert ctl.lease_ok(6) and not ctl.lease_ok(7)
-    assert not ctl.observe_validation(age=1, error=float("nan"))
-    assert not ctl.lease_ok(0)
+    ctl.record_mismatch(2, 0.05, t=5)        # intervals other than 1 do not count yet
+    assert not ctl.licensed
+    ctl.record_mismatch(1, 0.05, t=4)
+    assert ctl.licensed and ctl.interval.gap == 2
+    ctl.record_mismatch(2, 0.1, t=6)         # rate 0.05 < tau: the interval grows by 2
+    assert ctl.interval.gap == 4
+    ctl.record_mismatch(4, 0.8, t=10)        # rate 0.2: the interval is kept
+    assert ctl.interval.gap == 4
+    ctl.record_mismatch(4, float("nan"), t=14)   # ignored
+    ctl.record_mismatch(0, 0.01, t=14)
+    assert ctl.interval.gap == 4 and ctl.budget.rate_count == 2
+    assert ctl.record_refinement_error(age=3, error=0.05)
+    assert ctl.refinement_usable(5) and not ctl.refinement_usable(6)
+    assert ctl.record_refinement_error(age=2, error=0.05)   # the lease span grows by 2
+    assert ctl.refinement_usable(6) and not ctl.refinement_usable(7)
+    assert not ctl.record_refinement_error(age=1, error=float("nan"))
+    assert not ctl.refinement_usable(0)
+    assert ctl.record_refinement_error(age=1, error=0.01)   # the span restarts at 2
+    assert ctl.refinement_usable(3) and not ctl.refinement_usable(4)
+
+
+def test_controller_licensing_waits_for_the_prefix_floor():
+    ctl = Controller(ScheduleConfig(num_steps=20, tau=0.1, prefix_floor=5))
+    for t in (1, 2, 3):
+        ctl.record_mismatch(1, 0.01, t=t)
+    assert not ctl.licensed                  # passes before the floor do not license
+    ctl.record_mismatch(1, 0.01, t=5)
+    assert ctl.licensed
 
 
 def test_controller_budget_pacing():
     ctl = Controller(ScheduleConfig(num_steps=50, tau=0.1, budget=10, tail_exact=2))
-    ctl.license()
-    ctl.computed = 4
+    ctl.start_reuse()
+    ctl.budget.computed = 4
     # 10 - 4 - 2 = 4 computations left for steps 20..47: every 7 steps
-    assert ctl.pacing_gap(20) == 7
-    assert ctl.allowed_gap(20) == 2
-    ctl.next_gap = 12
-    assert ctl.allowed_gap(20) == 7
+    assert ctl.budget.pace(20) == 7
+    assert ctl.reuse_span(20) == 2
+    ctl.interval.gap = 12
+    assert ctl.reuse_span(20) == 7
+    # a mismatch rate above its running mean shortens the pace: mean 0.05, latest 0.1
+    ctl.budget.note_rate(0.0)
+    ctl.budget.note_rate(0.1)
+    assert ctl.budget.pace(20) == 4          # round(7 * 0.05 / 0.1) = round(3.5) = 4
     assert ctl.in_exact_tail(48) and not ctl.in_exact_tail(47)
-    ctl.computed = 8
-    assert ctl.mid_budget_exhausted() and not ctl.budget_exhausted()
+    ctl.budget.computed = 8
+    assert ctl.budget_spent_before_tail() and not ctl.budget_spent()
+    assert ctl.half_budget_spent()
+    assert ctl.budget.pace(20) is None       # nothing left before the tail
+    with pytest.raises(RuntimeError):
+        Controller(ScheduleConfig()).reuse_span(0)
 
 
 def test_reuse_extrapolation_is_exact_on_a_linear_trajectory():
