@@ -139,8 +139,8 @@ def step_sequence(wl, layers: int, steps: int, refresh_at: tuple, drift: float) 
         cfg = OperatorConfig(head_density=wl.density, host_banks=host)
         op = cls.build(cfg, geometry, n_layers=layers)
         if host:
-            op.preallocate_host(layers, wl.heads, wl.dim)
             op.record_copies = True
+            op.preallocate_host(layers, wl.heads, wl.dim)
         times, outs = [], None
         for step, (q, k, v) in enumerate(step_inputs()):
             kind = REFRESH if step in refresh_at else SPARSE
@@ -159,16 +159,18 @@ def step_sequence(wl, layers: int, steps: int, refresh_at: tuple, drift: float) 
                 f"{times[-1][1]:.1f} ms")
         copy_ms = 0.0
         host_bytes = 0
+        counts = {}
         if host:
-            copy_ms = sum(a.elapsed_time(b) for _, a, b in op.copy_events)
-            host_bytes = op.peak_bank_bytes()
             op.finish()
+            copy_ms, _ = op.copy_time()
+            host_bytes = op.peak_bank_bytes()
+            counts = op.pager_counts()
         del op
         torch.cuda.empty_cache()
-        return times, copy_ms, host_bytes, outs.clone()
+        return times, copy_ms, host_bytes, outs.clone(), counts
 
-    t_host, copy_ms, host_bytes, out_host = run(HostBankOperator, True)
-    t_gpu, _, _, out_gpu = run(Operator, False)
+    t_host, copy_ms, host_bytes, out_host, counts = run(HostBankOperator, True)
+    t_gpu, _, _, out_gpu, _ = run(Operator, False)
     total_host = sum(t for _, t in t_host)
     total_gpu = sum(t for _, t in t_gpu)
     exposed = max(0.0, total_host - total_gpu)
@@ -184,6 +186,7 @@ def step_sequence(wl, layers: int, steps: int, refresh_at: tuple, drift: float) 
         "exposed_copy_ms": round(exposed, 2),
         "copy_overlap_fraction": round(1.0 - exposed / copy_ms, 4) if copy_ms > 0 else None,
         "host_bank_bytes": host_bytes,
+        "pager_counts": counts,
         "outputs_identical": bool(torch.equal(out_host, out_gpu)),
     }
 

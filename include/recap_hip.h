@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define RECAP_ABI_VERSION 4
+#define RECAP_ABI_VERSION 5
 
 enum { RECAP_OK = 0, RECAP_EINVAL = 1, RECAP_EUNSUPPORTED = 2, RECAP_EHIP = 3 };
 enum { RECAP_F16 = 1, RECAP_BF16 = 2 };
@@ -280,6 +280,59 @@ int recap_refresh_capture_noalloc(const void* dense_out, int dtype, int64_t batc
                                   const int32_t* rowmap, int64_t n_tokens, int64_t n_video,
                                   void* det, float* dl, const float* glref,
                                   const float* center, float* stats, void* stream);
+
+/* Host-bank pager -------------------------------------------------------------------- */
+
+/* Refinement banks of n_keys (stream, layer) keys held in pinned host memory
+ * (hipHostMalloc, allocated on a key's first write-back or by recap_pager_reserve) and staged
+ * through n_slots device slots.  A bank is n_fields byte ranges of the given sizes (the
+ * operator pages value fp16 [banks, R, dim], log_mass fp32 [banks, R], partition
+ * [B, H, nb, nb], kernel mask [banks, tb, tb] and the drift reference fp32 [banks, R]); a
+ * slot's device fields are owned by the caller and bound once.  The pager owns a prefetch
+ * and a write-back stream (non-blocking, default priority) and the events that fence every
+ * reuse of a slot and of a key's host copy.  RECAP_PAGER_TIMING times every copy batch
+ * (recap_pager_copy_time).  One pager is driven by one host thread; destroying it waits
+ * for its transfers.
+ * Replaces HostBankOperator's slots, pinned banks, streams and events,
+ * recap/host_banks.py:45-56, 60-103, 200-262. */
+typedef struct recap_pager recap_pager;
+#define RECAP_PAGER_TIMING 1
+int recap_pager_create(int64_t n_keys, int32_t n_slots, const int64_t* field_bytes,
+                       int32_t n_fields, int32_t flags, recap_pager** out);
+int recap_pager_destroy(recap_pager* pager);
+int recap_pager_bind(recap_pager* pager, int32_t slot, void* const* device_fields);
+/* Allocate the pinned host banks of keys 0 .. n_keys-1 now.
+ * Replaces HostBankOperator.preallocate_host, recap/host_banks.py:85-97. */
+int recap_pager_reserve(recap_pager* pager, int64_t n_keys);
+/* Make key's bank the contents of slot for the work queued next on `stream` (the compute
+ * stream): waits for a prefetch of that key into that slot, else copies it on `stream` after
+ * the slot's pending write-back.  The key must hold a bank.
+ * Replaces _stage_in, recap/host_banks.py:200-207. */
+int recap_pager_stage_in(recap_pager* pager, int64_t key, int32_t slot, void* stream);
+/* Copy key's bank into slot on the prefetch stream once the compute stream has released the
+ * slot and its last write-back is done; a key with no bank is skipped.
+ * Replaces _maybe_prefetch, recap/host_banks.py:209-225. */
+int recap_pager_prefetch(recap_pager* pager, int64_t key, int32_t slot);
+/* Copy slot's contents into key's host bank on the write-back stream after the work queued
+ * so far on `stream`; the key then holds a bank.
+ * Replaces _stage_out and _split_out, recap/host_banks.py:132-146, 227-242. */
+int recap_pager_stage_out(recap_pager* pager, int64_t key, int32_t slot, void* stream);
+/* The work queued so far on `stream` is the slot's last use before it may be refilled.
+ * Replaces the slot_free event, recap/host_banks.py:194-196. */
+int recap_pager_release(recap_pager* pager, int32_t slot, void* stream);
+/* Wait for every transfer in flight.  Replaces finish, recap/host_banks.py:246-258. */
+int recap_pager_finish(recap_pager* pager);
+/* 1 if key holds a bank, 0 if not, -1 for bad arguments.  Host only. */
+int recap_pager_stored(const recap_pager* pager, int64_t key);
+/* Pinned host bytes allocated (-1 for a NULL pager).
+ * Replaces peak_bank_bytes, recap/host_banks.py:270-276. */
+int64_t recap_pager_host_bytes(const recap_pager* pager);
+/* counts[4]: stage-ins served by a prefetch, stage-ins copied on the compute stream,
+ * prefetches issued, stage-outs.  Host only; no counterpart in the reference. */
+int recap_pager_counts(const recap_pager* pager, int64_t* counts);
+/* Total milliseconds of the timed copy batches and their number (RECAP_PAGER_TIMING);
+ * waits for them.  No counterpart in the reference (its copies are untimed). */
+int recap_pager_copy_time(recap_pager* pager, double* total_ms, int64_t* copies);
 
 /* Asynchronous copy of a refinement bank between pinned host memory and the device on
  * `stream` (hipMemcpyAsync, direction inferred).

@@ -11,12 +11,13 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "librecap_hip.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 RECAP_OK, RECAP_EINVAL, RECAP_EUNSUPPORTED, RECAP_EHIP = 0, 1, 2, 3
 RECAP_F16, RECAP_BF16 = 1, 2
 CLOSURE_ROT, CLOSURE_CVK, CLOSURE_SCATTER = 1, 2, 4
 CAPTURE_NOALLOC_MAX_PAIRS = 1 << 19  # RECAP_CAPTURE_NOALLOC_MAX_PAIRS
+PAGER_TIMING = 1  # RECAP_PAGER_TIMING
 
 _P, _I64, _I, _F = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
 _STRIDES = [_I64, _I64, _I64]
@@ -61,6 +62,20 @@ SIGNATURES: dict[str, tuple] = {
                                    _I64, _I64, _P, _P, _P, _P, _P, _P, _P]),
     "recap_refresh_capture_noalloc": (_I, [_P, _I, _I64, _I64, _I64, *_STRIDES, _P, _P, _P,
                                            _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P]),
+    "recap_pager_create": (_I, [_I64, ctypes.c_int32, _P, ctypes.c_int32, ctypes.c_int32,
+                                _P]),
+    "recap_pager_destroy": (_I, [_P]),
+    "recap_pager_bind": (_I, [_P, ctypes.c_int32, _P]),
+    "recap_pager_reserve": (_I, [_P, _I64]),
+    "recap_pager_stage_in": (_I, [_P, _I64, ctypes.c_int32, _P]),
+    "recap_pager_prefetch": (_I, [_P, _I64, ctypes.c_int32]),
+    "recap_pager_stage_out": (_I, [_P, _I64, ctypes.c_int32, _P]),
+    "recap_pager_release": (_I, [_P, ctypes.c_int32, _P]),
+    "recap_pager_finish": (_I, [_P]),
+    "recap_pager_stored": (_I, [_P, _I64]),
+    "recap_pager_host_bytes": (_I64, [_P]),
+    "recap_pager_counts": (_I, [_P, _P]),
+    "recap_pager_copy_time": (_I, [_P, _P, _P]),
     "recap_bank_copy_async": (_I, [_P, _P, _I64, _P]),
 }
 

@@ -610,6 +610,106 @@ int recap_refresh_capture_noalloc(const void* dense_out, int dtype, int64_t batc
   return RECAP_OK;
 }
 
+// Host-bank pager ------------------------------------------------------------------------
+
+static Pager* as_pager(recap_pager* p) { return reinterpret_cast<Pager*>(p); }
+static const Pager* as_pager(const recap_pager* p) { return reinterpret_cast<const Pager*>(p); }
+
+static int check_slot_key(const Pager* p, int64_t key, int32_t slot) {
+  REQUIRE(p != nullptr, "pager is NULL");
+  REQUIRE(slot >= 0 && slot < pager_slots(p), "slot %d outside 0..%d", (int)slot,
+          pager_slots(p) - 1);
+  REQUIRE(key >= 0 && key < pager_keys(p), "key %lld outside 0..%lld", (long long)key,
+          (long long)pager_keys(p) - 1);
+  REQUIRE(pager_bound(p, slot), "slot %d has no bound device fields", (int)slot);
+  return RECAP_OK;
+}
+
+int recap_pager_create(int64_t n_keys, int32_t n_slots, const int64_t* field_bytes,
+                       int32_t n_fields, int32_t flags, recap_pager** out) {
+  REQUIRE(out != nullptr && field_bytes != nullptr, "NULL pointer");
+  REQUIRE(n_keys >= 1 && n_slots >= 1 && n_slots <= 8, "n_keys >= 1 and 1 <= n_slots <= 8");
+  REQUIRE(n_fields >= 1 && n_fields <= 16, "1 <= n_fields <= 16");
+  for (int32_t f = 0; f < n_fields; ++f)
+    REQUIRE(field_bytes[f] >= 0, "field %d has a negative size", (int)f);
+  REQUIRE((flags & ~RECAP_PAGER_TIMING) == 0, "unknown pager flags %d", (int)flags);
+  Pager* p = nullptr;
+  CHECK(hip_status(pager_create(n_keys, n_slots, field_bytes, n_fields,
+                                (flags & RECAP_PAGER_TIMING) != 0, &p), "pager create"));
+  *out = reinterpret_cast<recap_pager*>(p);
+  return RECAP_OK;
+}
+
+int recap_pager_destroy(recap_pager* pager) {
+  pager_destroy(as_pager(pager));
+  return RECAP_OK;
+}
+
+int recap_pager_bind(recap_pager* pager, int32_t slot, void* const* device_fields) {
+  Pager* p = as_pager(pager);
+  REQUIRE(p != nullptr && device_fields != nullptr, "NULL pointer");
+  REQUIRE(slot >= 0 && slot < pager_slots(p), "slot %d outside 0..%d", (int)slot,
+          pager_slots(p) - 1);
+  for (int f = 0; f < pager_fields(p); ++f)
+    REQUIRE(device_fields[f] != nullptr, "device field %d is NULL", f);
+  pager_bind(p, slot, device_fields);
+  return RECAP_OK;
+}
+
+int recap_pager_reserve(recap_pager* pager, int64_t n_keys) {
+  REQUIRE(pager != nullptr && n_keys >= 0, "bad arguments");
+  return hip_status(pager_reserve(as_pager(pager), n_keys), "pinned host allocation");
+}
+
+int recap_pager_stage_in(recap_pager* pager, int64_t key, int32_t slot, void* stream) {
+  CHECK(check_slot_key(as_pager(pager), key, slot));
+  REQUIRE(pager_stored(as_pager(pager), key), "key %lld holds no bank yet", (long long)key);
+  return hip_status(pager_stage_in(as_pager(pager), key, slot, as_stream(stream)), "stage_in");
+}
+
+int recap_pager_prefetch(recap_pager* pager, int64_t key, int32_t slot) {
+  CHECK(check_slot_key(as_pager(pager), key, slot));
+  if (!pager_stored(as_pager(pager), key)) return RECAP_OK;  // nothing to bring in yet
+  return hip_status(pager_prefetch(as_pager(pager), key, slot), "prefetch");
+}
+
+int recap_pager_stage_out(recap_pager* pager, int64_t key, int32_t slot, void* stream) {
+  CHECK(check_slot_key(as_pager(pager), key, slot));
+  return hip_status(pager_stage_out(as_pager(pager), key, slot, as_stream(stream)), "stage_out");
+}
+
+int recap_pager_release(recap_pager* pager, int32_t slot, void* stream) {
+  Pager* p = as_pager(pager);
+  REQUIRE(p != nullptr && slot >= 0 && slot < pager_slots(p), "bad pager or slot");
+  return hip_status(pager_release(p, slot, as_stream(stream)), "release");
+}
+
+int recap_pager_finish(recap_pager* pager) {
+  REQUIRE(pager != nullptr, "pager is NULL");
+  return hip_status(pager_finish(as_pager(pager)), "finish");
+}
+
+int recap_pager_stored(const recap_pager* pager, int64_t key) {
+  const Pager* p = as_pager(pager);
+  if (p == nullptr || key < 0 || key >= pager_keys(p)) return -1;
+  return pager_stored(p, key) ? 1 : 0;
+}
+
+int64_t recap_pager_host_bytes(const recap_pager* pager) {
+  return pager == nullptr ? -1 : pager_host_bytes(as_pager(pager));
+}
+
+int recap_pager_counts(const recap_pager* pager, int64_t* counts) {
+  REQUIRE(pager != nullptr && counts != nullptr, "NULL pointer");
+  pager_counts(as_pager(pager), counts);
+  return RECAP_OK;
+}
+
+int recap_pager_copy_time(recap_pager* pager, double* total_ms, int64_t* copies) {
+  REQUIRE(pager != nullptr && total_ms != nullptr && copies != nullptr, "NULL pointer");
+  return hip_status(pager_copy_time(as_pager(pager), total_ms, copies), "copy timing");
+}
+
 int recap_bank_copy_async(void* dst, const void* src, int64_t bytes, void* stream) {
   REQUIRE(dst && src, "NULL pointer");
   REQUIRE(bytes >= 0, "negative size");

@@ -136,4 +136,26 @@ hipError_t capture_scratch_pointer(float** out);
 hipError_t run_drift_center(const float* part, int banks, int tiles, int rows, float* center,
                             hipStream_t s);
 
+// Host-bank pager (pager.hip): pinned host banks, device slots, prefetch and write-back
+// streams.  Slot and key indices are checked by the caller (abi.hip).
+struct Pager;
+hipError_t pager_create(int64_t n_keys, int n_slots, const int64_t* field_bytes, int n_fields,
+                        bool timing, Pager** out);
+void pager_destroy(Pager* p);
+int pager_slots(const Pager* p);
+int64_t pager_keys(const Pager* p);
+int pager_fields(const Pager* p);
+bool pager_bound(const Pager* p, int slot);
+bool pager_stored(const Pager* p, int64_t key);
+int64_t pager_host_bytes(const Pager* p);
+void pager_counts(const Pager* p, int64_t* out4);
+void pager_bind(Pager* p, int slot, void* const* fields);
+hipError_t pager_reserve(Pager* p, int64_t n_keys);
+hipError_t pager_stage_in(Pager* p, int64_t key, int slot, hipStream_t s);
+hipError_t pager_prefetch(Pager* p, int64_t key, int slot);
+hipError_t pager_stage_out(Pager* p, int64_t key, int slot, hipStream_t s);
+hipError_t pager_release(Pager* p, int slot, hipStream_t s);
+hipError_t pager_finish(Pager* p);
+hipError_t pager_copy_time(Pager* p, double* total_ms, int64_t* n);
+
 }  // namespace recap

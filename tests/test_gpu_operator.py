@@ -199,19 +199,10 @@ def test_host_banks_multi_step_schedule_identical(cuda, layers):
     inputs = [tuple(perturb(x, 0.03, seed=i, step=step) for i, x in enumerate(base))
               for step in range(len(schedule))]
     runs = {}
-    sync_split = []  # split-state copies queued on the compute stream by the prefetching run
+    counts = {}
     for label, kw in [("gpu", {}), ("host", {"host_banks": True}),
                       ("host-noprefetch", {"host_banks": True, "prefetch": False})]:
         op, _ = build(wl, layers=layers, **kw)
-        if label == "host":
-            copy_split = op._copy_split
-
-            def counted(key_id, stream=None, _inner=copy_split):
-                if stream is None:
-                    sync_split.append(key_id)
-                return _inner(key_id, stream)
-
-            op._copy_split = counted
         outs, stats = [], []
         for step, kind in enumerate(schedule):
             op.begin_step(step, kind)
@@ -221,6 +212,7 @@ def test_host_banks_multi_step_schedule_identical(cuda, layers):
                 stats.append(op.drain_validation())
         if hasattr(op, "finish"):
             op.finish()
+            counts[label] = op.pager_counts()
         torch.cuda.synchronize()
         runs[label] = (outs, stats)
     for label in ("host", "host-noprefetch"):
@@ -228,9 +220,20 @@ def test_host_banks_multi_step_schedule_identical(cuda, layers):
             assert torch.equal(a, b), (label, i)
         assert runs["gpu"][1] == runs[label][1], label
     assert runs["gpu"][1][1] is not None  # the second refresh scored the first refinement
-    # With prefetch, a layer's split state arrives with its bank on the prefetch stream;
-    # only a layer nothing was prefetched for (layer 0 of a step, at most) copies it itself.
-    assert len(sync_split) <= len(schedule), sync_split
+    print(f"  pager counts {counts}", flush=True)
+    # Every bank a layer reads after the first refresh is staged in.  With prefetch all come
+    # from the prefetch stream except the very first, and, with an odd number of layers,
+    # each step's layer 0 (it shares a slot with the last layer, so it cannot be fetched
+    # during it); without prefetch all are copied on the compute stream.  Each refresh
+    # writes every layer's bank back.
+    steps_with_loads = len(schedule) - 1
+    loads = layers * steps_with_loads
+    assert counts["host"]["written_back"] == counts["host-noprefetch"]["written_back"] \
+        == layers * schedule.count(REFRESH)
+    assert counts["host-noprefetch"]["from_prefetch"] == 0
+    assert counts["host-noprefetch"]["copied"] == loads
+    assert counts["host"]["from_prefetch"] + counts["host"]["copied"] == loads
+    assert counts["host"]["copied"] == (1 if layers % 2 == 0 else steps_with_loads)
 
 
 @pytest.mark.parametrize("name,heads", [("wan2.1-480p", 2), ("cogvideox1.5", 2),
