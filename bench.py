@@ -191,6 +191,41 @@ def step_sequence(wl, layers: int, steps: int, refresh_at: tuple, drift: float) 
     }
 
 
+def refresh_calls(wl, count: int) -> dict:
+    """A first REFRESH (selection, basis, capture) and then ``count`` revalidating REFRESH
+    calls on inputs drifted 3% each, which score the previous refinement, select again and
+    decide the rerank; per-call wall time from HIP events (one JSON object)."""
+    import torch
+
+    from recap_amd import Operator, OperatorConfig, REFRESH
+    from recap_amd.layout import Layout, SparseGeometry, hilbert_permutation
+    from recap_amd.synthetic import make_qkv, perturb
+
+    dev = torch.device("cuda:0")
+    layout = Layout.from_permutation(hilbert_permutation(wl.grid), text_tokens=wl.text_tokens,
+                                     text_first=wl.text_first)
+    op = Operator.build(OperatorConfig(head_density=wl.density), SparseGeometry.build(layout, 128),
+                        n_layers=1)
+    x = make_qkv(wl, seed=0, device=dev)
+    times = []
+    for call in range(count + 1):
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        op.begin_step(call, REFRESH)
+        op.attend(0, *x)
+        end.record()
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(end))
+        log(f"[refresh] call {call}: {times[-1]:.1f} ms")
+        x = tuple(perturb(t, 0.03, seed=i, step=call + 1) for i, t in enumerate(x))
+    age, error = op.drain_validation()
+    return {"refresh": f"{wl.name}: a first REFRESH, then {count} revalidating REFRESH calls "
+                       "(3% drift each)", "first_ms": round(times[0], 2),
+            "revalidating_ms": [round(t, 2) for t in times[1:]], "last_validation_error":
+            round(error, 6)}
+
+
 def cpu_baseline(op, q1, k1, v1, wl, heads: int) -> dict:
     """The oracle's sparse call on the host for ``heads`` of the heads (all query blocks),
     timed with the operator's refinement state; heads are independent and cost the same,
@@ -261,6 +296,10 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=20, help="layers of the step sequence")
     ap.add_argument("--no-sequence", action="store_true",
                     help="skip the paged step sequence of the default run")
+    ap.add_argument("--refresh", type=int, default=0, metavar="K",
+                    help="run only K revalidating REFRESH calls after a first one (the "
+                         "selection, the capture with validation, the rerank overlap) and "
+                         "print their timing; a profiling target for those kernels")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: --gpus {args.gpus} is not supported in this build "
@@ -285,6 +324,9 @@ def main() -> int:
     dev = torch.device("cuda:0")
     if args.sequence:
         print(json.dumps(step_sequence(wl, args.layers, 10, (0, 5), 0.03)), flush=True)
+        return 0
+    if args.refresh > 0:
+        print(json.dumps(refresh_calls(wl, args.refresh)), flush=True)
         return 0
     log(f"[bench] workload {wl.name}: heads={wl.heads} d={wl.dim} N={wl.tokens}")
     q0, k0, v0 = make_qkv(wl, seed=0, device=dev)

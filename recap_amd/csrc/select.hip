@@ -5,8 +5,7 @@
 //                  masks are reproducible bit for bit.
 //   topk           top-`keep` key blocks per query block (recap/sparse/router.py:20-22),
 //                  ties to the lower block index, plus the forced trailing partial block
-//                  (recap/sparse/attention.py:88-94); one workgroup per row, bitonic sort
-//                  of (monotone score key, index) pairs in LDS.
+//                  (recap/sparse/attention.py:88-94); a radix select per row, one wave.
 //   kernel_mask    video partition embedded in the kernel's block grid with every row and
 //                  column from the dense start on (recap/kernels/block_sparse.py:52-75).
 //   mask_overlap   |P_new & P_old| and |P_new| for the rerank decision
@@ -64,53 +63,106 @@ hipError_t run_block_scores(const ScoreArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Top-k by radix select, one wave per row.  Scores become order-preserving 32-bit keys
+// (flip all bits of a negative float, set the sign bit of a positive one); four passes over
+// the 8-bit digits from the most significant down find the key T of the keep-th largest
+// score exactly: each pass histograms, in LDS, the digit of the keys that match the digits
+// fixed so far, and a wave-wide suffix scan over the 256 buckets picks the digit whose
+// bucket holds the keep-th key.  The row then takes every key above T and, of the keys equal
+// to T, as many as are still needed in ascending block order (ties to the lower index),
+// counted with one ballot per 64 blocks.  A row of nb scores is read once and its partition
+// row written once; the keys stay in registers (PER per lane).
 constexpr int kMaxSortBlocks = 4096;
+constexpr int kTopkWaves = 4;
 
-__global__ __launch_bounds__(256) void topk_kernel(TopkArgs a) {
-  __shared__ unsigned long long key[kMaxSortBlocks];
-  __shared__ uint8_t sel[kMaxSortBlocks];
-  const int row = blockIdx.x % a.nb, bank = blockIdx.x / a.nb;
-  const int t = threadIdx.x;
-  const float* s = a.scores + ((int64_t)bank * a.nb + row) * a.nb;
-  int P = 1;
-  while (P < a.nb) P <<= 1;
-  for (int j = t; j < P; j += 256) {
-    unsigned long long k = 0ull;
-    if (j < a.nb) {
-      const unsigned bits = __float_as_uint(s[j]);
-      const unsigned mono = (bits >> 31) ? ~bits : (bits | 0x80000000u);
-      k = ((unsigned long long)mono << 32) | (unsigned long long)(0xffffffffu - (unsigned)j);
-    }
-    key[j] = k;
-    sel[j] = 0;
+__device__ inline unsigned order_key(float x) {
+  const unsigned bits = __float_as_uint(x);
+  return (bits >> 31) ? ~bits : (bits | 0x80000000u);
+}
+
+template <int PER>
+__global__ __launch_bounds__(64 * kTopkWaves) void topk_kernel(TopkArgs a) {
+  __shared__ unsigned hist[kTopkWaves][256];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t rows = (int64_t)a.banks * a.nb;
+  const int64_t row_id = (int64_t)blockIdx.x * kTopkWaves + wave;
+  const bool live = row_id < rows;        // a wave past the last row counts nothing
+  const int nb = a.nb;
+  const float* s = a.scores + (live ? row_id : 0) * nb;
+  unsigned key[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int j = lane + 64 * i;
+    key[i] = (live && j < nb) ? order_key(s[j]) : 0u;
   }
-  __syncthreads();
-  for (int size = 2; size <= P; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = t; i < P; i += 256) {
-        const int p = i ^ stride;
-        if (p > i) {
-          const unsigned long long x = key[i], y = key[p];
-          const bool desc = (i & size) == 0;
-          if (desc ? (x < y) : (x > y)) { key[i] = y; key[p] = x; }
-        }
+  unsigned* h = hist[wave];
+  unsigned prefix = 0, fixed = 0;   // digits found so far, and their bit mask
+  int need = a.keep;                // keys still to take at or below the current prefix
+  for (int shift = 24; shift >= 0; shift -= 8) {
+#pragma unroll
+    for (int b = lane; b < 256; b += 64) h[b] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int j = lane + 64 * i;
+      if (live && j < nb && (key[i] & fixed) == prefix) atomicAdd(&h[(key[i] >> shift) & 255], 1u);
+    }
+    __syncthreads();
+    // Lane l owns buckets 255-4l .. 252-4l (descending digits); scan the lanes in order.
+    unsigned c[4], own = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) { c[k] = h[255 - 4 * lane - k]; own += c[k]; }
+    unsigned above = own;   // inclusive prefix over lanes 0..lane
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const unsigned v = __shfl_up(above, off, 64);
+      if (lane >= off) above += v;
+    }
+    above -= own;           // keys in buckets above this lane's
+    int digit = -1;
+    unsigned before = above;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (digit < 0 && before < (unsigned)need && (unsigned)need <= before + c[k]) {
+        digit = 255 - 4 * lane - k;
+        above = before;
       }
-      __syncthreads();
+      before += c[k];
     }
+    // Exactly one bucket holds the keep-th key (none in a wave past the last row).
+    const unsigned long long owner = __ballot(digit >= 0);
+    const int src = owner ? __ffsll((long long)owner) - 1 : 0;
+    digit = owner ? __shfl(digit, src, 64) : 0;
+    above = owner ? __shfl(above, src, 64) : 0u;
+    prefix |= (unsigned)digit << shift;
+    fixed |= 0xffu << shift;
+    need -= (int)above;
+    __syncthreads();   // the histogram is read by every lane before the next pass clears it
   }
-  for (int i = t; i < a.keep; i += 256) {
-    sel[0xffffffffu - (unsigned)(key[i] & 0xffffffffull)] = 1;
-  }
-  __syncthreads();
-  uint8_t* out = a.partition + ((int64_t)bank * a.nb + row) * a.nb;
-  const bool full_row = a.force_last && row == a.nb - 1;
-  for (int j = t; j < a.nb; j += 256) {
-    out[j] = (sel[j] || full_row || (a.force_last && j == a.nb - 1)) ? 1 : 0;
+  // prefix is now the keep-th largest key; `need` keys equal to it are taken, lowest first.
+  const unsigned long long below = lane ? (~0ull >> (64 - lane)) : 0ull;
+  const int row = (int)(row_id % nb);
+  const bool full_row = a.force_last && row == nb - 1;
+  uint8_t* out = a.partition + (live ? row_id : 0) * nb;
+  int taken = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int j = lane + 64 * i;
+    const bool valid = live && j < nb;
+    const bool tie = valid && key[i] == prefix;
+    const unsigned long long ties = __ballot(tie);
+    const bool pick = valid && (key[i] > prefix || (tie && taken + __popcll(ties & below) < need));
+    taken += __popcll(ties);
+    if (valid) out[j] = (pick || full_row || (a.force_last && j == nb - 1)) ? 1 : 0;
   }
 }
 
 hipError_t run_topk(const TopkArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(topk_kernel, dim3((unsigned)(a.banks * a.nb)), dim3(256), 0, s, a);
+  const int64_t rows = (int64_t)a.banks * a.nb;
+  const dim3 grid((unsigned)((rows + kTopkWaves - 1) / kTopkWaves)), block(64 * kTopkWaves);
+  if (a.nb <= 256) hipLaunchKernelGGL(topk_kernel<4>, grid, block, 0, s, a);
+  else if (a.nb <= 1024) hipLaunchKernelGGL(topk_kernel<16>, grid, block, 0, s, a);
+  else hipLaunchKernelGGL(topk_kernel<kMaxSortBlocks / 64>, grid, block, 0, s, a);
   return hipGetLastError();
 }
 

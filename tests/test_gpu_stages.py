@@ -65,6 +65,31 @@ def test_stage1_pool_scores_masks_bit_exact(cuda, name, heads):
     assert torch.equal(part1, part) and torch.equal(kmask1, kmask)
 
 
+@pytest.mark.parametrize("nb", [1, 63, 64, 65, 256, 257, 929, 1024, 1025, 4096])
+def test_topk_radix_select_with_ties_vs_oracle(cuda, nb):
+    """The radix-select top-k against the oracle's stable sort on rows built to tie: plain
+    normal scores, a handful of integer values, fully tied rows, signed zeros among tiny
+    values; random keep, the forced partial block on and off; every size class of the
+    kernel (up to 256, 1024 and 4096 blocks per row)."""
+    g = torch.Generator().manual_seed(nb)
+    banks = 3
+    scores = torch.randn(banks, nb, nb, generator=g)
+    scores[0, ::3] = torch.randint(-3, 3, (len(range(0, nb, 3)), nb), generator=g).float()
+    scores[1, ::4] = 1.5
+    tiny = torch.randn(nb, generator=g) * 1e-30
+    tiny[::5] = 0.0
+    tiny[1::7] = -0.0
+    scores[2, ::2] = tiny
+    for keep in sorted({1, max(1, nb // 5), max(1, nb // 2), nb}):
+        for force_last in (False, True):
+            got = K.topk_blocks(scores.to(cuda), keep, force_last).cpu()
+            want = O.topk_mask(scores, keep)
+            if force_last:
+                want[:, :, -1] = True
+                want[:, -1, :] = True
+            assert torch.equal(got, want), (nb, keep, force_last)
+
+
 @pytest.mark.parametrize("name", list(SMALL))
 def test_kv_pack_tile_images(cuda, name):
     wl, (q, k, v), (qg, kg, vg), rowmap, fwd, geo = _setup(name, None, cuda)
