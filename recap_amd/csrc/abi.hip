@@ -568,6 +568,8 @@ int recap_refresh_capture(const void* dense_out, int dtype, int64_t batch, int64
                      n_video, det, dl, glref, center, stats, a, work));
   const bool validate = glref != nullptr;
   REQUIRE(!validate || stat_partial, "validation needs stat_partial");
+  REQUIRE(!validate || (reinterpret_cast<uintptr_t>(stat_partial) & 7) == 0,
+          "stat_partial must be 8-byte aligned");
   if (!work) return RECAP_OK;
   a.stat_part = stat_partial;
   int blocks = 0;

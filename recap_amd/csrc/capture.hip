@@ -144,19 +144,25 @@ hipError_t capture_scratch_pointer(float** out) {
   return hipSuccess;
 }
 
-// out2 = fixed-order sums of n (a, b) pairs.
-__global__ __launch_bounds__(256) void sum_pairs_kernel(const float* part, int n, float* out2) {
-  __shared__ float ra[256], rb[256];
-  const int t = threadIdx.x, per = (n + 255) / 256;
+// out2 = fixed-order sums of n (a, b) pairs: thread t adds pairs t, t + 1024, t + 2048, ...
+// in turn (coalesced loads), then a fixed tree over the threads.
+constexpr int kSumThreads = 1024;
+
+__global__ __launch_bounds__(kSumThreads) void sum_pairs_kernel(const float* part, int n, float* out2) {
+  __shared__ float ra[kSumThreads], rb[kSumThreads];
+  const int t = threadIdx.x;
+  const f32x2* pairs = reinterpret_cast<const f32x2*>(part);
   float sa = 0.0f, sb = 0.0f;
-  for (int i = t * per; i < min((t + 1) * per, n); ++i) {
-    sa += part[2 * (int64_t)i];
-    sb += part[2 * (int64_t)i + 1];
+#pragma unroll 8
+  for (int i = t; i < n; i += kSumThreads) {
+    const f32x2 v = pairs[i];
+    sa += v[0];
+    sb += v[1];
   }
   ra[t] = sa;
   rb[t] = sb;
   __syncthreads();
-  for (int h = 128; h >= 1; h >>= 1) {
+  for (int h = kSumThreads / 2; h >= 1; h >>= 1) {
     if (t < h) { ra[t] += ra[t + h]; rb[t] += rb[t + h]; }
     __syncthreads();
   }
@@ -164,7 +170,7 @@ __global__ __launch_bounds__(256) void sum_pairs_kernel(const float* part, int n
 }
 
 hipError_t run_sum_pairs(const float* part, int n, float* out2, hipStream_t s) {
-  hipLaunchKernelGGL(sum_pairs_kernel, dim3(1), dim3(256), 0, s, part, n, out2);
+  hipLaunchKernelGGL(sum_pairs_kernel, dim3(1), dim3(kSumThreads), 0, s, part, n, out2);
   return hipGetLastError();
 }
 
