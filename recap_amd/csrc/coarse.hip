@@ -191,10 +191,13 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
   const int short_reg = 4 * (short_slot >> 3) + (short_slot & 3);
   const float short_lane = g == ((short_slot >> 2) & 1) ? short2 / c1 : 0.0f;
 
-  // Table tiles (images written by the tables kernel) are copied verbatim into LDS, one
-  // tile ahead, by buffer loads over this bank's images; tiles with no omitted block are
-  // skipped.
-  // Stage layout: kbar image, vbar image, w image.
+  // Table tiles (images written by the tables kernel) are copied verbatim into LDS by
+  // buffer loads over this bank's images; tiles with no omitted block are skipped.  The
+  // loop is pipelined across tiles: while the softmax and p.vbar of tile t_i run, the
+  // q.kbar and qsq.w chains of t_{i+1} run on the matrix cores, so a wave's MFMAs overlap
+  // its own VALU work.  Tile t_i lives in stage i % 2 (layout: kbar, vbar, w images); its
+  // kbar and w images arrive two tiles ahead (they are read one tile ahead), its vbar image
+  // one tile ahead.
   const int bank_tab = ntiles * kTabBytes;
   const int64_t tab_elems = (int64_t)bank * ntiles * kCoarseSlots * D;
   const int64_t w_elems = (int64_t)bank * ntiles * (kWBytes / 2);
@@ -204,13 +207,12 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
       (void*)(a.w + w_elems), 0, ntiles * kWBytes, kBufferRsrcWord3);
   const __amdgpu_buffer_rsrc_t vrs =
       __builtin_amdgcn_make_buffer_rsrc((void*)(a.vbar + tab_elems), 0, bank_tab, kBufferRsrcWord3);
-  auto copy_tile = [&](int k, char* dst) {
+  auto copy_kw = [&](int k, char* dst) {  // kbar and w images of tile k
     const int off = __builtin_amdgcn_readfirstlane(k * kTabBytes);
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) {
       const int lo = 4096 * i + 1024 * wave, vo = 4096 * i + 16 * t;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void*)(dst + lo), 16, vo, off, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void*)(dst + kTabBytes + lo), 16, vo, off, 0, 0);
       if constexpr (!FOLD)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_void*)(dst + 2 * kTabBytes + lo), 16, vo, off, 0, 0);
     }
@@ -220,10 +222,76 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
                                                4 * t, woff, 0, 0);
     }
   };
-  auto next_tile = [&](int k) {
+  auto copy_v = [&](int k, char* dst) {  // vbar image of tile k
+    const int off = __builtin_amdgcn_readfirstlane(k * kTabBytes);
+#pragma unroll
+    for (int i = 0; i < NDMA; ++i) {
+      const int lo = 4096 * i + 1024 * wave, vo = 4096 * i + 16 * t;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void*)(dst + kTabBytes + lo), 16, vo, off, 0, 0);
+    }
+  };
+  // This wave's copies into LDS have landed and every wave has passed the same point.
+  auto tile_barrier = [&]() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0x7 << 4);  // vmcnt(0) lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  // Operands of the bias MFMA that starts each tile's q.kbar accumulator: A[slot][0] = -inf
+  // for a kept slot, 0 for an omitted one; B[0][row] = 1; every other element of A and B is
+  // 0, so no -inf meets a 0.  The product is -inf on the kept slots and +0 on the omitted
+  // ones, where the chain then runs exactly as from a zero accumulator; a kept slot stays
+  // -inf through the chain and gets p = exp2(-inf) = 0 with no per-score select.
+  const unsigned bias_kept = g == 0 ? pack2<T>(-INFINITY, 0.0f) : 0u;
+  const u32x4 bias_ones = u32x4{g == 0 ? pack2<T>(1.0f, 0.0f) : 0u, 0u, 0u, 0u};
+  // The omitted-block words in registers (lane i of ow_lo / ow_hi holds the word of tile i /
+  // 64 + i) and the tiles that have one as bit masks on the scalar unit, so the walk reads
+  // no LDS for its bookkeeping.
+  const unsigned ow_lo = lane < ntiles ? omit[lane] : 0u;
+  const unsigned ow_hi = 64 + lane < ntiles ? omit[64 + lane] : 0u;
+  const unsigned long long ne_lo = __ballot(ow_lo != 0), ne_hi = __ballot(ow_hi != 0);
+  auto next_tile = [&](int k) {  // the first tile after k with an omitted block, or ntiles
     ++k;
-    while (k < ntiles && omit[k] == 0) ++k;
-    return k;
+    if (k < 64) {
+      const unsigned long long m = ne_lo >> k;
+      if (m) return k + (int)__builtin_ctzll(m);
+      k = 64;
+    }
+    if (k < 128) {
+      const unsigned long long m = ne_hi >> (k - 64);
+      if (m) return k + (int)__builtin_ctzll(m);
+    }
+    return ntiles;
+  };
+  // Omitted-block word of tile k (0 past the last tile).
+  auto omit_word = [&](int k) -> unsigned {
+    if (k >= ntiles) return 0u;
+    return k < 64 ? (unsigned)__builtin_amdgcn_readlane((int)ow_lo, k)
+                  : (unsigned)__builtin_amdgcn_readlane((int)ow_hi, k - 64);
+  };
+
+  // The score chains of the tile in stage `st`: s = q.kbar from the bias, quad = qsq.w.
+  // MFMA i of the chain: 0 the bias; folded, 1 the quad and 2 .. NS+1 the q.kbar slices;
+  // full, q.kbar slice s at 2s+1 and qsq.w slice s at 2s+2 (each chain in slice order).
+  constexpr int kScoreMfmas = FOLD ? NS + 2 : 2 * NS + 1;
+  auto score_frag = [&](const char* st, int i) {  // A operand of MFMA i >= 1
+    if constexpr (FOLD) {
+      return i == 1 ? lds_load16(st + 2 * kTabBytes, 32 * l32 + 16 * g)
+                    : lds_load16(st, G::k_off(l32, 2 * (i - 2) + g));
+    } else {
+      return lds_load16(st + ((i - 1) & 1 ? 2 * kTabBytes : 0), G::k_off(l32, 2 * ((i - 1) >> 1) + g));
+    }
+  };
+  auto score_mfma = [&](int i, const u32x4& f, const u32x4& bias_a, f32x16& sacc, f32x16& wacc) {
+    if (i == 0) {
+      sacc = T::mfma32(bias_a, bias_ones, f32x16{});
+    } else if constexpr (FOLD) {
+      if (i == 1) wacc = T::mfma32(f, qsq_pk[0], wacc);
+      else sacc = T::mfma32(f, qreg[i - 2], sacc);
+    } else {
+      if ((i - 1) & 1) wacc = T::mfma32(f, qsq_pk[(i - 1) >> 1], wacc);
+      else sacc = T::mfma32(f, qreg[(i - 1) >> 1], sacc);
+    }
   };
 
   // Running max m2 (log2 units), raised lazily: a tile's probabilities are first taken
@@ -237,76 +305,11 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) oacc[dt] = f32x16{};
 
-  // Tile k from stage `cur` while the next tile is copied into stage `nxt`.
-  auto tile = [&](int k, const char* cur, char* nxt) {
-    // This wave's copies of tile k have landed and every wave is done with the other stage.
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt(0x7 << 4);  // vmcnt(0) lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    const int kn = next_tile(k);
-    if (kn < ntiles) copy_tile(kn, nxt);
-
-    const char* kb_lds = cur;
-    const char* vt_lds = kb_lds + kTabBytes;
-    const char* w_lds = kb_lds + 2 * kTabBytes;
-    const unsigned ow = __builtin_amdgcn_readfirstlane(omit[k]);
-    // The two independent chains s = q.kbar and quad = qsq.w (NS MFMAs each, chunk 2 s + g
-    // of both tiles) interleaved, each slice reading its fragments two slices ahead, so no
-    // MFMA waits on an LDS read issued just before it.
-    f32x16 sacc = f32x16{}, wacc = f32x16{};
-    if constexpr (FOLD) {
-      // quad = qsq'.w' over the kFoldCols folded features: one MFMA; then the q.kbar chain.
-      wacc = T::mfma32(lds_load16(w_lds, 32 * l32 + 16 * g), qsq_pk[0], wacc);
-      u32x4 kf[3];
-#pragma unroll
-      for (int s = 0; s < 2; ++s) kf[s] = lds_load16(kb_lds, G::k_off(l32, 2 * s + g));
-#pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        if (s + 2 < NS) kf[(s + 2) % 3] = lds_load16(kb_lds, G::k_off(l32, 2 * (s + 2) + g));
-        sacc = T::mfma32(kf[s % 3], qreg[s], sacc);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    } else {
-      u32x4 kf[3], wf[3];
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        kf[s] = lds_load16(kb_lds, G::k_off(l32, 2 * s + g));
-        wf[s] = lds_load16(w_lds, G::k_off(l32, 2 * s + g));
-      }
-#pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        if (s + 2 < NS) {
-          kf[(s + 2) % 3] = lds_load16(kb_lds, G::k_off(l32, 2 * (s + 2) + g));
-          wf[(s + 2) % 3] = lds_load16(w_lds, G::k_off(l32, 2 * (s + 2) + g));
-        }
-        sacc = T::mfma32(kf[s % 3], qreg[s], sacc);
-        wacc = T::mfma32(wf[s % 3], qsq_pk[s], wacc);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-    // V-bar fragments of the PV product, read now so they are in registers after the softmax.
-    u32x4 vf[NDT][2];
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
-        vf[dt][hh] = lds_load16(vt_lds, coarse_vt_off(32 * dt + l32, 8 * (2 * hh + g)));
-
-    // Lane (g, l32) holds slots mfma_row(rr, g): bits 8 (rr / 4) + 4 g + rr % 4 of the word,
-    // the same for the 32 lanes of a half-wave, so each slot's omitted flag is a wave mask
-    // built on the scalar unit; kept blocks get p = 0 (a select after the exp).  The
-    // log-count ln 128 common to every full block is left out of the scores and added to
-    // the LSE at the end (softmax, gated share and output do not depend on it); a short
-    // last block gets log2(n / 128) in its own tile.
-    auto omitted = [&](int rr) {
-      const int sh = 8 * (rr >> 2) + (rr & 3);
-      return __builtin_amdgcn_inverse_ballot_w64(
-          (((ow >> sh) & 1u) ? 0x00000000ffffffffull : 0ull) |
-          (((ow >> (sh + 4)) & 1u) ? 0xffffffff00000000ull : 0ull));
-    };
-    // The short last block's log2(n / 128), moved into its q.kbar score (units of c1) so the
-    // loops below stay free of it.
+  // Lane (g, l32) holds slots mfma_row(rr, g); kept slots hold s = -inf.  The log-count
+  // ln 128 common to every full block is left out of the scores and added to the LSE at the
+  // end (softmax, gated share and output do not depend on it); the short last block gets
+  // its log2(n / 128) added to its q.kbar score (units of c1).
+  auto short_fix = [&](int k, f32x16& sacc) {
     if (k == last_tile && short2 != 0.0f) {
       int sreg = short_reg;
       asm volatile("" : "+s"(sreg));  // keeps the 16 compares in this rare branch
@@ -314,31 +317,62 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
       for (int rr = 0; rr < 16; ++rr)
         if (rr == sreg) sacc[rr] += short_lane;
     }
-    float p[16];
-    float part = 0.0f, gpart = 0.0f;
-    // Probabilities against m2: score - m2 = c1 s + (gate ? c2 quad : 0) - m2, the gate
-    // term and -m2 folded into one select.
-    auto probs = [&]() __attribute__((always_inline)) {
-      part = 0.0f;
-      gpart = 0.0f;
+  };
+  // Probability of slot register rr against m2: score - m2 = c1 s + (gate ? c2 quad : 0) - m2,
+  // the gate term and -m2 folded into one select; part and gpart accumulate in rr order.
+  auto prob = [&](int rr, const f32x16& sacc, const f32x16& wacc, float* p, float& part,
+                  float& gpart) {
+    const bool gate = wacc[rr] <= thq;
+    const float tm = gate ? fmaf(wacc[rr], c2, -m2) : -m2;
+    p[rr] = __builtin_amdgcn_exp2f(fmaf(sacc[rr], c1, tm));
+    part += p[rr];
+    gpart += gate ? p[rr] : 0.0f;
+  };
+
+  // The score chains of the tile in stage `st` (omitted word ow) into sn/wn.  With a
+  // softmax to do (`probs`), the first pass of the probabilities of the current tile's
+  // scores (sacc/wacc) is spread over the chain: each MFMA is followed by one or two slots'
+  // probabilities, so the wave issues them while the MFMA runs (the chain's MFMAs depend
+  // on each other), and the A operands are read from LDS two MFMAs ahead.
+  auto scores = [&](const char* st, unsigned ow, f32x16& sn, f32x16& wn, auto probs,
+                    const f32x16& sacc, const f32x16& wacc, float* p, float& part,
+                    float& gpart) {
+    // Lane (g, l32) holds A[slot l32][8g .. 8g+7] of the bias MFMA.
+    const u32x4 bias_a = u32x4{(ow >> l32) & 1u ? 0u : bias_kept, 0u, 0u, 0u};
+    u32x4 f[3];
+    f[1] = score_frag(st, 1);
+    f[2] = score_frag(st, 2);
+    wn = f32x16{};
+    part = 0.0f;
+    gpart = 0.0f;
 #pragma unroll
-      for (int rr = 0; rr < 16; ++rr) {
-        const bool gate = wacc[rr] <= thq;
-        const float tm = gate ? fmaf(wacc[rr], c2, -m2) : -m2;
-        const float e = __builtin_amdgcn_exp2f(fmaf(sacc[rr], c1, tm));
-        p[rr] = omitted(rr) ? e : 0.0f;
-        part += p[rr];
-        gpart += gate ? p[rr] : 0.0f;
+    for (int i = 0; i < kScoreMfmas; ++i) {
+      if (i >= 1 && i + 2 < kScoreMfmas) f[(i + 2) % 3] = score_frag(st, i + 2);
+      score_mfma(i, f[i % 3], bias_a, sn, wn);
+      if constexpr (decltype(probs)::value) {
+#pragma unroll
+        for (int rr = 16 * i / kScoreMfmas; rr < 16 * (i + 1) / kScoreMfmas; ++rr)
+          prob(rr, sacc, wacc, p, part, gpart);
       }
-    };
-    probs();
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // The rest of tile k after the first pass of its probabilities: the check of their sums
+  // (and the redo with a raised m2), the running sums and the p.vbar product (vbar image in
+  // stage `st`).
+  auto finish_tile = [&](const char* st, const f32x16& sacc, const f32x16& wacc, float* p,
+                         float part, float gpart) {
+    const char* vt_lds = st + kTabBytes;
     if (__any(!(part <= kSumCap))) {
-      // Raise m2 to the running max over this tile's omitted slots (both lanes of a row).
+      // Raise m2 to the running max over this tile's omitted slots (both lanes of a row; a
+      // kept slot's score is -inf).  On the first tile, where m2 = -inf, the kept slots gave
+      // p = NaN (-inf + inf) above, which also lands here.
       float mx = -INFINITY;
 #pragma unroll
       for (int rr = 0; rr < 16; ++rr) {
         const float sc = fmaf(sacc[rr], c1, wacc[rr] <= thq ? wacc[rr] * c2 : 0.0f);
-        mx = __builtin_elementwise_maximum(mx, omitted(rr) ? sc : -INFINITY);
+        mx = __builtin_elementwise_maximum(mx, sc);
       }
       mx = pair_max(mx);
       if (mx > m2) {
@@ -349,7 +383,10 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
         for (int dt = 0; dt < NDT; ++dt) oacc[dt] *= alpha;
         m2 = mx;
       }
-      probs();
+      part = 0.0f;
+      gpart = 0.0f;
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) prob(rr, sacc, wacc, p, part, gpart);
     }
     lsum += part;
     gsum += gpart;
@@ -361,15 +398,52 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) oacc[dt] = T::mfma32(vf[dt][hh], pk[hh], oacc[dt]);
-    return kn;
+      for (int hh = 0; hh < 2; ++hh)
+        oacc[dt] = T::mfma32(lds_load16(vt_lds, coarse_vt_off(32 * dt + l32, 8 * (2 * hh + g))),
+                             pk[hh], oacc[dt]);
+  };
+
+  // One step i: tile k = t_i (scores in sacc/wacc, vbar in stage `cur`) and the scores of
+  // kn = t_{i+1} (kbar/w in stage `nxt`).  Copies issued: kbar/w of t_{i+2} into `cur`
+  // (its kbar/w, those of t_i, were read in step i-1) and vbar of t_{i+1} into `nxt` (its
+  // vbar, that of t_{i-1}, was read in step i-1).  Past the last tile the scores computed
+  // are of stale LDS contents and unused.  Returns t_{i+2}.
+  f32x16 sacc, wacc;
+  auto step = [&](int k, int kn, char* cur, char* nxt) {
+    tile_barrier();
+    const int kn2 = kn < ntiles ? next_tile(kn) : ntiles;
+    if (kn2 < ntiles) copy_kw(kn2, cur);
+    if (kn < ntiles) copy_v(kn, nxt);
+    short_fix(k, sacc);
+    f32x16 sn, wn;
+    float p[16], part, gpart;
+    scores(nxt, omit_word(kn), sn, wn, std::true_type{}, sacc, wacc, p, part, gpart);
+    finish_tile(cur, sacc, wacc, p, part, gpart);
+    sacc = sn;
+    wacc = wn;
+    return kn2;
   };
   int k = next_tile(-1);
-  if (k < ntiles) copy_tile(k, st0);
-  while (k < ntiles) {
-    k = tile(k, st0, st1);
-    if (k >= ntiles) break;
-    k = tile(k, st1, st0);
+  if (k < ntiles) {
+    int kn = next_tile(k);
+    copy_kw(k, st0);
+    copy_v(k, st0);
+    if (kn < ntiles) copy_kw(kn, st1);
+    tile_barrier();
+    {
+      float p[16], part, gpart;
+      scores(st0, omit_word(k), sacc, wacc, std::false_type{}, sacc, wacc, p, part, gpart);
+    }
+    while (true) {
+      int kn2 = step(k, kn, st0, st1);
+      if (kn >= ntiles) break;
+      k = kn;
+      kn = kn2;
+      kn2 = step(k, kn, st1, st0);
+      if (kn >= ntiles) break;
+      k = kn;
+      kn = kn2;
+    }
   }
 
   // Value drift s C_vk q in the output layout: stage C_vk over the tables' LDS.
