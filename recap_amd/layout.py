@@ -19,17 +19,19 @@ from . import kernels
 
 
 def validate_permutation(permutation: np.ndarray, grid: Sequence[int]) -> np.ndarray:
-    """Check a reordered-position -> native-index permutation (recap/sparse/geometry.py:13-24)."""
-    grid = tuple(int(x) for x in grid)
-    n = int(np.prod(grid))
-    permutation = np.asarray(permutation, dtype=np.int64)
-    if permutation.shape != (n,):
-        raise ValueError(f"permutation shape {permutation.shape} != ({n},)")
-    if permutation.min(initial=0) != 0 or permutation.max(initial=-1) != n - 1:
-        raise ValueError("permutation is outside [0, prod(grid))")
-    if np.unique(permutation).size != n:
-        raise ValueError("permutation is not one-to-one")
-    return permutation
+    """The permutation (reordered position -> native index) as int64, after checking that it
+    maps the prod(grid) positions one-to-one onto [0, prod(grid)); ValueError otherwise
+    (the contract of recap/sparse/geometry.py:13-24)."""
+    n = math.prod(int(x) for x in grid)
+    perm = np.asarray(permutation, dtype=np.int64)
+    if perm.ndim != 1 or perm.size != n:
+        raise ValueError(f"permutation has shape {perm.shape}, expected ({n},)")
+    if n and (perm.min() < 0 or perm.max() >= n):
+        raise ValueError(f"permutation values leave [0, {n})")
+    # Every index in range appears exactly once iff no index is hit twice.
+    if n and np.bincount(perm, minlength=n).max() > 1:
+        raise ValueError("permutation repeats an index")
+    return perm
 
 
 def hilbert_permutation(grid: Sequence[int]) -> np.ndarray:
@@ -41,10 +43,18 @@ def hilbert_permutation(grid: Sequence[int]) -> np.ndarray:
 
 @dataclass
 class Layout:
-    """Reorder/restore of a native sequence (recap/sparse/layout.py:11-92)."""
+    """A native token sequence seen as [Hilbert-ordered video | text] (the contract of
+    recap/sparse/layout.py:11-92).  The attribute names are the reference's: the model
+    integrations set ``text_tokens`` per prompt and then clear ``_gather_cache``
+    (recap/models/hunyuan.py:30-39).
+
+    Everything derives from one forward map, forward[r] = native token of reordered row r
+    (video rows first, then text), which is also the kernels' int32 row map; the backward
+    map is its inverse.
+    """
 
     permutation: torch.Tensor  # reordered video position -> native video position
-    inverse: torch.Tensor
+    inverse: torch.Tensor      # native video position -> reordered video position
     video_tokens: int
     text_tokens: int
     text_first: bool
@@ -53,68 +63,64 @@ class Layout:
     @classmethod
     def from_permutation(cls, permutation, *, text_tokens: int, text_first: bool) -> "Layout":
         p = torch.as_tensor(permutation, dtype=torch.long, device="cpu")
-        if p.ndim != 1 or torch.unique(p).numel() != p.numel():
+        n = p.numel()
+        ok = p.ndim == 1 and (n == 0 or (int(p.min()) >= 0 and int(p.max()) < n
+                                         and int(torch.bincount(p, minlength=n).max()) == 1))
+        if not ok:
             raise ValueError("invalid layout permutation")
-        return cls(permutation=p, inverse=torch.argsort(p), video_tokens=p.numel(),
+        inverse = torch.empty_like(p)
+        inverse[p] = torch.arange(n)
+        return cls(permutation=p, inverse=inverse, video_tokens=n,
                    text_tokens=int(text_tokens), text_first=bool(text_first))
 
     @property
     def video_offset(self) -> int:
+        """Native position of the first video token."""
         return self.text_tokens if self.text_first else 0
 
     @property
     def tokens(self) -> int:
         return self.video_tokens + self.text_tokens
 
-    def _gather_indices(self, device) -> tuple[torch.Tensor, torch.Tensor]:
-        key = f"gather:{device}"
-        cached = self._gather_cache.get(key)
-        if cached is not None:
-            return cached
-        nv, tt = self.video_tokens, self.text_tokens
-        text = torch.arange(tt, dtype=torch.long)
-        if self.text_first:
-            fwd = torch.cat((self.permutation + tt, text))
-            inv = torch.cat((text + nv, self.inverse))
-        else:
-            fwd = torch.cat((self.permutation, text + nv))
-            inv = torch.cat((self.inverse, text + nv))
-        pair = (fwd.to(device), inv.to(device))
-        self._gather_cache[key] = pair
-        return pair
+    def _cached(self, what: str, device, make):
+        key = (what, str(device))
+        if key not in self._gather_cache:
+            self._gather_cache[key] = make()
+        return self._gather_cache[key]
+
+    def _maps(self, device) -> tuple[torch.Tensor, torch.Tensor]:
+        """(forward, backward) on ``device``: forward[r] is the native token of reordered
+        row r, backward[t] the reordered row of native token t."""
+        def make():
+            text_start = 0 if self.text_first else self.video_tokens
+            forward = torch.cat((self.permutation + self.video_offset,
+                                 torch.arange(self.text_tokens) + text_start))
+            backward = torch.empty_like(forward)
+            backward[forward] = torch.arange(forward.numel())
+            return forward.to(device), backward.to(device)
+        return self._cached("maps", device, make)
 
     def rowmap(self, device) -> torch.Tensor:
-        """int32 [tokens]: native token of each reordered row, on ``device`` (cached)."""
-        key = f"rowmap:{device}"
-        cached = self._gather_cache.get(key)
-        if cached is None:
-            fwd, _ = self._gather_indices("cpu")
-            cached = fwd.to(torch.int32).to(device)
-            self._gather_cache[key] = cached
-        return cached
+        """int32 [tokens]: the forward map on ``device``, as the kernels read it."""
+        return self._cached("rowmap", device,
+                            lambda: self._maps("cpu")[0].to(torch.int32).to(device))
 
     def video_permutation(self, device) -> torch.Tensor:
-        key = f"video:{device}"
-        cached = self._gather_cache.get(key)
-        if cached is None:
-            cached = self.permutation.to(device)
-            self._gather_cache[key] = cached
-        return cached
+        return self._cached("video", device, lambda: self.permutation.to(device))
 
     def _check(self, x: torch.Tensor) -> None:
-        if x.shape[-2] != self.video_tokens + self.text_tokens:
-            raise ValueError(f"sequence {x.shape[-2]} != video+text "
-                             f"{self.video_tokens + self.text_tokens}")
+        if x.shape[-2] != self.tokens:
+            raise ValueError(f"sequence {x.shape[-2]} != video+text {self.tokens}")
 
     def reorder(self, x: torch.Tensor) -> torch.Tensor:
         """Native model order -> [reordered video | text]."""
         self._check(x)
-        return x.index_select(-2, self._gather_indices(x.device)[0])
+        return x.index_select(-2, self._maps(x.device)[0])
 
     def restore(self, x: torch.Tensor) -> torch.Tensor:
         """[reordered video | text] -> native model order."""
         self._check(x)
-        return x.index_select(-2, self._gather_indices(x.device)[1])
+        return x.index_select(-2, self._maps(x.device)[1])
 
 
 @dataclass

@@ -20,6 +20,7 @@ the reference's, so the diffusers processors call it unchanged.
 
 from __future__ import annotations
 
+import dataclasses
 import math
 from dataclasses import dataclass, field
 
@@ -34,6 +35,7 @@ from .layout import Layout, SparseGeometry
 EXACT = "exact"
 REFRESH = "refresh"
 SPARSE = "sparse"
+_KINDS = (EXACT, REFRESH, SPARSE)
 
 
 class SparseAttention:
@@ -92,7 +94,9 @@ class SparseAttention:
 
 @dataclass
 class DetailBank:
-    """One layer's cached refinement and its partition (recap/operator.py:33-59)."""
+    """One layer's cached refinement and its partition.  The field names and layouts are
+    the reference's (recap/operator.py:33-59): host paging and the model integrations
+    read them."""
 
     head_kernel_mask: torch.Tensor | None = None  # [banks, tb, tb] bool
     partition: torch.Tensor | None = None         # [B, H, nb, nb] bool
@@ -101,16 +105,23 @@ class DetailBank:
     coarse_lse: torch.Tensor | None = None        # [banks, rows] fp32
     valid: bool = False
     refreshed_at: int = 0
-    pending_stats: torch.Tensor | None = None     # [2] fp32
+    pending_stats: torch.Tensor | None = None     # [2] fp32: sum sq error, sum sq output
     pending_age: int | None = None
 
     def release(self) -> None:
-        self.head_kernel_mask = self.partition = None
-        self.value = self.log_mass = self.coarse_lse = None
-        self.valid = False
-        self.refreshed_at = 0
-        self.pending_stats = None
-        self.pending_age = None
+        """Forget the refinement: every field back to its declared default."""
+        for f in dataclasses.fields(self):
+            setattr(self, f.name, f.default)
+
+    def take_pending(self) -> tuple[torch.Tensor, int] | None:
+        """The error statistics a refresh left for the controller, cleared as they are read."""
+        stats, age = self.pending_stats, self.pending_age
+        self.pending_stats = self.pending_age = None
+        return None if stats is None or age is None else (stats, int(age))
+
+    def refinement_bytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in (self.value, self.log_mass)
+                   if t is not None)
 
 
 class BankChunk:
@@ -190,52 +201,63 @@ class Operator:
     _forced_partition: torch.Tensor | None = None
     _forced_rerank: bool | None = None
 
+    # The per-(stream, layer) state is a grid of cells: the sparse state in ``layers`` and
+    # the refinement in ``banks``, both indexed [stream][layer] (the reference's indexing,
+    # which host paging and the integrations use).  The current call is the cursor
+    # (kind, step, stream, refreshed_layers), set by begin_step / set_stream.
+
     def __post_init__(self) -> None:
-        if not self.layers or isinstance(self.layers[0], SparseAttention):
+        rows = self.layers
+        if not rows or not all(isinstance(row, (list, tuple)) and row for row in rows):
             raise TypeError("Operator.layers must be indexed [stream][layer]")
-        self.banks = [[DetailBank() for _ in row] for row in self.layers]
+        self.banks = [[DetailBank() for _ in row] for row in rows]
 
     @classmethod
     def build(cls, config: OperatorConfig, geometry: SparseGeometry, *, n_layers: int,
               n_streams: int = 1) -> "Operator":
-        if n_layers < 1 or n_streams < 1:
+        """A fresh sparse state in every cell (recap/operator.py:176-191)."""
+        if min(n_layers, n_streams) < 1:
             raise ValueError("n_layers and n_streams must be positive")
-        layers = [[SparseAttention(geometry, config) for _ in range(n_layers)]
-                  for _ in range(n_streams)]
-        return cls(config, geometry.layout, layers)
+        grid = [[SparseAttention(geometry, config) for _ in range(n_layers)]
+                for _ in range(n_streams)]
+        return cls(config, geometry.layout, grid)
 
     @property
     def n_streams(self) -> int:
         return len(self.layers)
 
+    def _cells(self):
+        """Every (sparse state, bank) pair, stream by stream."""
+        for states, banks in zip(self.layers, self.banks):
+            yield from zip(states, banks)
+
+    def _start_call(self, kind: str, step: int) -> None:
+        self.kind, self.step, self.stream, self.refreshed_layers = kind, int(step), 0, 0
+
     def reset(self) -> None:
-        for row in self.banks:
-            for bank in row:
-                bank.release()
-        for row in self.layers:
-            for layer in row:
-                layer.reset()
-        self.kind = EXACT
-        self.step = 0
-        self.stream = 0
-        self.refreshed_layers = 0
+        """Back to the state right after build (recap/operator.py:197-210)."""
+        for state, bank in self._cells():
+            state.reset()
+            bank.release()
         for state in self._chunk_states.values():
             state.reset()
+        self._start_call(EXACT, 0)
 
     @property
     def banks_valid(self) -> bool:
-        return bool(self.banks) and all(bank.valid for row in self.banks for bank in row)
+        """Every layer of every stream holds a refinement."""
+        flags = [bank.valid for _, bank in self._cells()]
+        return bool(flags) and all(flags)
 
     def begin_step(self, step: int, kind: str) -> None:
-        if kind not in (EXACT, REFRESH, SPARSE):
+        """Start the calls of one computed step (stream 0 first)."""
+        if kind not in _KINDS:
             raise ValueError(f"unknown computed call kind {kind!r}")
-        self.step = int(step)
-        self.kind = kind
-        self.stream = 0
-        self.refreshed_layers = 0
+        self._start_call(kind, step)
 
     def set_stream(self, stream: int) -> None:
-        if not 0 <= stream < self.n_streams:
+        """Select the stream (CFG branch) the next calls belong to."""
+        if stream not in range(self.n_streams):
             raise ValueError(f"stream {stream} outside 0..{self.n_streams - 1}")
         self.stream = int(stream)
 
@@ -454,27 +476,16 @@ class Operator:
     # -- the refinement error ------------------------------------------------------------
 
     def drain_validation(self) -> tuple[int, float] | None:
-        """Relative RMS error over all layers and the smallest refinement age
-        (recap/operator.py:531-547)."""
-        stats, ages = [], []
-        for row in self.banks:
-            for bank in row:
-                if bank.pending_stats is not None and bank.pending_age is not None:
-                    stats.append(bank.pending_stats)
-                    ages.append(int(bank.pending_age))
-                bank.pending_stats = None
-                bank.pending_age = None
-        if not stats:
+        """(smallest refinement age, relative RMS error over all layers) of the refreshes
+        since the last drain, or None (recap/operator.py:531-547).  The error pools every
+        layer's sums: sqrt(sum sq error / sum sq output)."""
+        pending = [p for p in (bank.take_pending() for _, bank in self._cells()) if p]
+        if not pending:
             return None
-        numerator, denominator = (float(x) for x in torch.stack(stats).sum(dim=0))
-        error = math.sqrt(numerator / denominator) if denominator > 0.0 else float("inf")
-        return min(ages), error
+        err_sq, out_sq = torch.stack([stats for stats, _ in pending]).sum(dim=0).tolist()
+        error = math.sqrt(err_sq / out_sq) if out_sq > 0.0 else float("inf")
+        return min(age for _, age in pending), error
 
     def peak_bank_bytes(self) -> int:
-        total = 0
-        for row in self.banks:
-            for bank in row:
-                for tensor in (bank.value, bank.log_mass):
-                    if tensor is not None:
-                        total += tensor.numel() * tensor.element_size()
-        return total
+        """Bytes of the refinement values and log-masses held on the device."""
+        return sum(bank.refinement_bytes() for _, bank in self._cells())
