@@ -124,62 +124,70 @@ class DetailBank:
                    if t is not None)
 
 
-class BankChunk:
-    """A DetailBank restricted to a range of banks (``bank_chunks``, recap/operator.py:62-145).
+_BANK_TENSORS = ("head_kernel_mask", "partition", "value", "log_mass", "coarse_lse")
 
-    Tensor fields read as views of the layer-wide tensors and write through into them;
-    the layer-level flags are published by ``commit`` after all groups have run.
-    """
 
-    _TENSORS = ("head_kernel_mask", "partition", "value", "log_mass", "coarse_lse")
+@dataclass(frozen=True)
+class _HeadGroup:
+    """Where one group of heads (``bank_chunks``, recap/operator.py:62-145, 260-326) sits in
+    a layer's bank tensors: banks lo..hi of total, heads head0..head1 of batch ``batch``."""
 
-    def __init__(self, bank: DetailBank, *, lo: int, hi: int, total: int, batch: int,
-                 head0: int, head1: int, heads: int):
-        object.__setattr__(self, "_bank", bank)
-        object.__setattr__(self, "_range", (lo, hi, total, batch, head0, head1, heads))
-        for name in ("valid", "refreshed_at", "pending_stats", "pending_age"):
-            object.__setattr__(self, name, getattr(bank, name))
+    lo: int
+    hi: int
+    total: int
+    batch: int
+    head0: int
+    head1: int
+    heads: int
 
-    def __getattr__(self, name):
-        if name in BankChunk._TENSORS:
-            lo, hi, _, batch, h0, h1, _ = self._range
-            whole = getattr(self._bank, name)
-            if whole is None:
-                return None
-            if name == "partition":
-                return whole[batch:batch + 1, h0:h1]
-            return whole[lo:hi]
-        return getattr(self._bank, name)
+    def rows(self, name: str, whole: torch.Tensor | None) -> torch.Tensor | None:
+        if whole is None:
+            return None
+        if name == "partition":  # [B, H, nb, nb]
+            return whole[self.batch:self.batch + 1, self.head0:self.head1]
+        return whole[self.lo:self.hi]
 
-    def __setattr__(self, name, value):
-        if name not in BankChunk._TENSORS:
-            object.__setattr__(self, name, value)
-            return
-        lo, hi, total, batch, h0, h1, heads = self._range
-        if value is None:
-            setattr(self._bank, name, None)
-            return
-        whole = getattr(self._bank, name)
+    def layer_shape(self, name: str, part: torch.Tensor) -> tuple:
         if name == "partition":
-            shape = (max(1, total // heads), heads, *value.shape[2:])
-        else:
-            shape = (total, *value.shape[1:])
-        if whole is None or tuple(whole.shape) != shape:
-            whole = torch.empty(shape, dtype=value.dtype, device=value.device)
-            setattr(self._bank, name, whole)
-        if name == "partition":
-            whole[batch:batch + 1, h0:h1] = value
-        else:
-            whole[lo:hi] = value
+            return (max(1, self.total // self.heads), self.heads, *part.shape[2:])
+        return (self.total, *part.shape[1:])
 
-    def commit(self, views: list["BankChunk"]) -> None:
-        bank = self._bank
-        bank.valid = self.valid
-        bank.refreshed_at = self.refreshed_at
-        bank.pending_age = self.pending_age
-        stats = [v.pending_stats for v in views if v.pending_stats is not None]
-        bank.pending_stats = None if not stats else (
-            stats[0] if len(stats) == 1 else torch.stack(stats).sum(dim=0))
+    def open(self, bank: DetailBank) -> DetailBank:
+        """The group's own DetailBank: the layer's tensors as views of the group's rows and a
+        copy of the layer-level flags."""
+        own = DetailBank(valid=bank.valid, refreshed_at=bank.refreshed_at,
+                         pending_stats=bank.pending_stats, pending_age=bank.pending_age)
+        for name in _BANK_TENSORS:
+            setattr(own, name, self.rows(name, getattr(bank, name)))
+        return own
+
+    def close(self, bank: DetailBank, own: DetailBank) -> None:
+        """Bring back the tensors the group's computation replaced (a view it wrote in place
+        needs nothing); a field it dropped is dropped for the layer."""
+        for name in _BANK_TENSORS:
+            part, whole = getattr(own, name), getattr(bank, name)
+            view = self.rows(name, whole)
+            if part is None:
+                if whole is not None:
+                    setattr(bank, name, None)
+                continue
+            if view is not None and part.data_ptr() == view.data_ptr() and part.shape == view.shape:
+                continue
+            shape = self.layer_shape(name, part)
+            if whole is None or tuple(whole.shape) != shape:
+                whole = torch.empty(shape, dtype=part.dtype, device=part.device)
+                setattr(bank, name, whole)
+            self.rows(name, whole).copy_(part)
+
+
+def _publish_groups(bank: DetailBank, groups: list[DetailBank]) -> None:
+    """Layer-level flags after all head groups ran: the last group's, with the validation
+    sums added over the groups."""
+    last = groups[-1]
+    bank.valid, bank.refreshed_at, bank.pending_age = last.valid, last.refreshed_at, last.pending_age
+    stats = [g.pending_stats for g in groups if g.pending_stats is not None]
+    bank.pending_stats = torch.stack(stats).sum(dim=0) if len(stats) > 1 else (
+        stats[0] if stats else None)
 
 
 @dataclass
@@ -330,7 +338,7 @@ class Operator:
             self._forced_rerank = kept / max(total, 1) < self.config.rerank_min_overlap
             forced = forced.reshape(b, h, geo.nb, geo.nb)
         per = max(1, math.ceil(h / chunks))
-        views: list[BankChunk] = []
+        opened: list[DetailBank] = []
         group = 0
         refreshed_before = self.refreshed_layers
         for bi in range(b):
@@ -341,9 +349,10 @@ class Operator:
                     state = SparseAttention(self.layers[self.stream][layer_index].geometry,
                                             self.config)
                     self._chunk_states[(self.stream, layer_index, group)] = state
-                view = BankChunk(bank, lo=bi * h + h0, hi=bi * h + h1, total=b * h, batch=bi,
-                                 head0=h0, head1=h1, heads=h)
-                views.append(view)
+                span = _HeadGroup(lo=bi * h + h0, hi=bi * h + h1, total=b * h, batch=bi,
+                                  head0=h0, head1=h1, heads=h)
+                view = span.open(bank)
+                opened.append(view)
                 qs, ks, vs = (x[bi:bi + 1, h0:h1] for x in (q, k, v))
                 self._forced_partition = (None if forced is None
                                           else forced[bi:bi + 1, h0:h1].reshape(-1, geo.nb, geo.nb))
@@ -357,11 +366,12 @@ class Operator:
                     self._refresh(state, view, qs, kv, geo, rowmap, out[bi:bi + 1, h0:h1],
                                   lse[bi:bi + 1, h0:h1],
                                   head=(head_all[0][lo:hi], head_all[1][lo:hi]), selection=sel)
+                span.close(bank, view)
                 group += 1
         self._forced_partition = None
         self._forced_rerank = None
-        if views:
-            views[-1].commit(views)
+        if opened:
+            _publish_groups(bank, opened)
         if self.refreshed_layers > refreshed_before:
             self.refreshed_layers = refreshed_before + 1
         return out
