@@ -34,15 +34,18 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
   constexpr int kWBytes = FOLD ? kCoarseSlots * kFoldCols * 2 : kTabBytes;
   constexpr int kStage = 2 * kTabBytes + kWBytes;  // kbar, vbar, w of one tile
   constexpr int NDMA = kTabBytes / 4096;           // 16-byte copies per thread per image
-  static_assert(2 * kStage >= kMatBytes, "a staged D x D matrix spans both stages");
+  static_assert(FOLD || 2 * kStage >= kMatBytes, "a staged D x D matrix spans both stages");
   static_assert(!FOLD || kWBytes == 1024, "a folded w tile is 4 bytes per thread");
   // Two tile stages in separate arrays, each access naming one of them at compile time: the
   // compiler can then tell that reads of one stage do not touch the copies filling the other,
   // and does not wait for those copies first.  A staged D x D matrix (U^T, C_vk) keeps rows
-  // 0 .. D/2-1 in stage 0 and the rest in stage 1 (same swizzle: it depends on the row's low
-  // bits only).
+  // 0 .. D/2-1 and the rest in two halves of the same swizzled layout (it depends on the row's
+  // low bits only): in the folded kernel in a buffer of its own (43.5 + 32 KB, still two
+  // workgroups per CU), so the first tiles arrive while qsq runs and C_vk while the tiles
+  // do; in the full one, whose stages are larger, over stages 0 and 1.
   __shared__ __attribute__((aligned(16))) char st0[kStage];
   __shared__ __attribute__((aligned(16))) char st1[kStage];
+  __shared__ __attribute__((aligned(16))) char mat[FOLD ? kMatBytes : 16];
   __shared__ unsigned omit[kMaxVideoBlocks / kCoarseSlots];
   __shared__ float wsum[4];
   __shared__ float feat[FOLD ? 4 * 32 * kFoldCols : 1];  // folded qsq features per row
@@ -53,18 +56,6 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
   const int bank = lin / a.qtiles, qt = lin % a.qtiles;
   const int b = bank / a.heads, h = bank % a.heads;
   const int ntiles = (a.nb + kCoarseSlots - 1) / kCoarseSlots;
-
-  // Omitted blocks of this query block (partition 0) as one bit word per table tile.
-  {
-    const uint8_t* prow = a.partition + ((int64_t)bank * a.nb + qt) * a.nb;
-    for (int base = 0; base < ntiles * kCoarseSlots; base += 256) {
-      const int j = base + t;
-      const unsigned long long bal = __ballot(j < a.nb && prow[j] == 0);
-      const int wi = (base + 64 * wave) / kCoarseSlots;
-      if (lane == 0 && wi < ntiles) omit[wi] = (unsigned)bal;
-      if (lane == 0 && wi + 1 < ntiles) omit[wi + 1] = (unsigned)(bal >> 32);
-    }
-  }
 
   // Stage a D x D matrix of the query type (row-major in HBM) into LDS by buffer loads into
   // LDS, all in flight at once: one wave instruction fills 1 KB of the swizzled image in lane
@@ -79,9 +70,11 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
       const int pos = 4096 * i + 16 * t;  // byte position in the half image
       const int row = pos / (2 * D), pc = (pos % (2 * D)) >> 4;
       const int from = row * 2 * D + ((pc ^ G::swz(row, NCH)) << 4);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(st0 + 4096 * i + 1024 * wave), 16,
+      char* lo = FOLD ? mat : st0;
+      char* hi = FOLD ? mat + kHalfBytes : st1;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(lo + 4096 * i + 1024 * wave), 16,
                                                from, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(st1 + 4096 * i + 1024 * wave), 16,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(hi + 4096 * i + 1024 * wave), 16,
                                                from + kHalfBytes, 0, 0, 0);
     }
   };
@@ -94,102 +87,47 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
   };
   // Fragment of row tile `rt` (32 rows) of a staged matrix; rt is a compile-time index.
   auto matrix_frag = [&](int rt, int chunk) {
-    return rt < NDT / 2 ? lds_load16(st0, G::k_off(32 * rt + l32, chunk))
-                        : lds_load16(st1, G::k_off(32 * (rt - NDT / 2) + l32, chunk));
+    if constexpr (FOLD)
+      return rt < NDT / 2 ? lds_load16(mat, G::k_off(32 * rt + l32, chunk))
+                          : lds_load16(mat + kMatBytes / 2, G::k_off(32 * (rt - NDT / 2) + l32, chunk));
+    else
+      return rt < NDT / 2 ? lds_load16(st0, G::k_off(32 * rt + l32, chunk))
+                          : lds_load16(st1, G::k_off(32 * (rt - NDT / 2) + l32, chunk));
   };
+  // U^T and this wave's row-map entry are requested before the partition row, so all three
+  // arrive in one wait.
   stage_matrix(a.u_t + (int64_t)bank * D * D);  // U^T
-
   const int r = qt * kBlock + wave * 32 + l32;  // always < rows
   const int nat = a.rowmap[r];
+
+  // Omitted blocks of this query block (partition 0) as one bit word per table tile.  All
+  // of the row's loads are issued before the first ballot, so the scan waits once, and the
+  // Q row (which waits only for the row-map entry) is requested in between.
   u32x4 qreg[NS];
   {
+    const uint8_t* prow = a.partition + ((int64_t)bank * a.nb + qt) * a.nb;
+    constexpr int kScan = kMaxVideoBlocks / 256;
+    uint8_t cell[kScan];
+#pragma unroll
+    for (int i = 0; i < kScan; ++i) cell[i] = prow[min(256 * i + t, a.nb - 1)];  // in the row
     const uint16_t* qrow = a.q + b * a.sB + h * a.sH + (int64_t)nat * a.sN;
 #pragma unroll
     for (int s = 0; s < NS; ++s) qreg[s] = *reinterpret_cast<const u32x4*>(qrow + 16 * s + 8 * g);
+    unsigned flags = 0;
+#pragma unroll
+    for (int i = 0; i < kScan; ++i)
+      if (256 * i + t < a.nb && cell[i] == 0) flags |= 1u << i;
+#pragma unroll
+    for (int i = 0; i < kScan; ++i) {
+      if (256 * i >= ntiles * kCoarseSlots) break;
+      const unsigned long long bal = __ballot((flags >> i) & 1u);
+      const int wi = (256 * i + 64 * wave) / kCoarseSlots;
+      if (lane == 0 && wi < ntiles) omit[wi] = (unsigned)bal;
+      if (lane == 0 && wi + 1 < ntiles) omit[wi + 1] = (unsigned)(bal >> 32);
+    }
   }
+
   staged_barrier();
-
-  // qsq = (U^T q)^2 in the query type (rotated value rounded, then its square rounded):
-  // lane (g, l32) holds dims 32 ot + mfma_row(rr, g) of its row.  Full form: qsq in the
-  // B-operand layout of the quadratic form (dims in swap23 order, as the w table's
-  // columns).  Folded form: the kFoldCols features [qsq_0 .. qsq_{r-1}, T_hi, T_mid, T_lo,
-  // 0 ...] as one B operand, gathered through LDS (lane (g, l32) holds features 8g .. 8g+7).
-  constexpr int kQsqRegs = FOLD ? 1 : NDT * 2;
-  u32x4 qsq_pk[kQsqRegs];
-  float* frow = feat + (wave * 32 + l32) * kFoldCols;
-  if constexpr (FOLD) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) frow[8 * g + e] = 0.0f;
-    __syncthreads();
-  }
-  float tail = 0.0f;
-#pragma unroll
-  for (int ot = 0; ot < NDT; ++ot) {
-    f32x16 acc = f32x16{};
-#pragma unroll
-    for (int s = 0; s < NS; ++s)
-      acc = T::mfma32(matrix_frag(ot, 2 * s + g), qreg[s], acc);
-    float sq[16];
-#pragma unroll
-    for (int rr = 0; rr < 16; ++rr) {
-      const float x = T::to_f(T::from_f(acc[rr]));
-      sq[rr] = T::to_f(T::from_f(x * x));
-    }
-    if constexpr (FOLD) {
-#pragma unroll
-      for (int rr = 0; rr < 16; ++rr) {
-        const int c = 32 * ot + mfma_row(rr, g);
-        if (c < a.rank) frow[c] = sq[rr];
-        else tail += sq[rr];
-      }
-    } else {
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
-        qsq_pk[2 * ot + hh] = u32x4{pack2<T>(sq[8 * hh], sq[8 * hh + 1]),
-                                    pack2<T>(sq[8 * hh + 2], sq[8 * hh + 3]),
-                                    pack2<T>(sq[8 * hh + 4], sq[8 * hh + 5]),
-                                    pack2<T>(sq[8 * hh + 6], sq[8 * hh + 7])};
-    }
-  }
-  if constexpr (FOLD) {
-    // T = sum_{c>=r} qsq_c over both lanes of the row, split into three bf16 parts.
-    const float total = pair_sum(tail);
-    const float hi = T::to_f(T::from_f(total));
-    const float mid = T::to_f(T::from_f(total - hi));
-    const float lo = T::to_f(T::from_f((total - hi) - mid));
-    if (g == 0) {
-      frow[a.rank] = hi;
-      frow[a.rank + 1] = mid;
-      frow[a.rank + 2] = lo;
-    }
-    __syncthreads();
-    const float* f8 = frow + 8 * g;
-    qsq_pk[0] = u32x4{pack2<T>(f8[0], f8[1]), pack2<T>(f8[2], f8[3]), pack2<T>(f8[4], f8[5]),
-                      pack2<T>(f8[6], f8[7])};
-  }
-  __syncthreads();  // the table tiles reuse the U^T staging area
-
-  const float s32 = a.scale;
-  const float ssq = (float)((double)a.scale * (double)a.scale);
-  const float half = (float)(0.5 * (double)a.scale * (double)a.scale);
-  const float thsq = (float)((double)a.theta * (double)a.theta);
-  // The gate fl(quad * s^2) <= theta^2 as one compare quad <= thq: fl(x * s^2) is monotone in
-  // x, so the quads that pass form (-inf, thq], with thq within an ulp or two of
-  // theta^2 / s^2 (found by stepping; exact for every scale, not only powers of two).
-  float thq = thsq / ssq;
-  for (int i = 0; i < 4 && thq * ssq > thsq; ++i) thq = nextafterf(thq, -INFINITY);
-  for (int i = 0; i < 4 && nextafterf(thq, INFINITY) * ssq <= thsq; ++i)
-    thq = nextafterf(thq, INFINITY);
-  // Scores in log2 units: c1 on q.kbar, c2 on the gated qsq.w term.
-  const float c1 = s32 * kLog2e, c2 = half * kLog2e;
-  const float ln_full = logf((float)kBlock);
-  const float short2 = (logf((float)(a.n_video - kBlock * (a.nb - 1))) - ln_full) * kLog2e;
-  const int last_tile = (a.nb - 1) / kCoarseSlots;
-  // Block nb - 1 sits in slot sl = mfma_row(short_reg, g) of the last tile for the lanes
-  // of half g = (sl / 4) % 2; those lanes add its log2(n / 128) in units of c1.
-  const int short_slot = (a.nb - 1) % kCoarseSlots;
-  const int short_reg = 4 * (short_slot >> 3) + (short_slot & 3);
-  const float short_lane = g == ((short_slot >> 2) & 1) ? short2 / c1 : 0.0f;
 
   // Table tiles (images written by the tables kernel) are copied verbatim into LDS by
   // buffer loads over this bank's images; tiles with no omitted block are skipped.  The
@@ -269,6 +207,100 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
     return k < 64 ? (unsigned)__builtin_amdgcn_readlane((int)ow_lo, k)
                   : (unsigned)__builtin_amdgcn_readlane((int)ow_hi, k - 64);
   };
+
+  // The first two tiles with an omitted block; the folded kernel copies their images now,
+  // while the qsq MFMAs run (both stages are free: U^T is in its own buffer).
+  const int k_first = next_tile(-1);
+  const int k_second = k_first < ntiles ? next_tile(k_first) : ntiles;
+  if constexpr (FOLD) {
+    if (k_first < ntiles) {
+      copy_kw(k_first, st0);
+      copy_v(k_first, st0);
+      if (k_second < ntiles) copy_kw(k_second, st1);
+    }
+  }
+
+  // qsq = (U^T q)^2 in the query type (rotated value rounded, then its square rounded):
+  // lane (g, l32) holds dims 32 ot + mfma_row(rr, g) of its row.  Full form: qsq in the
+  // B-operand layout of the quadratic form (dims in swap23 order, as the w table's
+  // columns).  Folded form: the kFoldCols features [qsq_0 .. qsq_{r-1}, T_hi, T_mid, T_lo,
+  // 0 ...] as one B operand, gathered through LDS (lane (g, l32) holds features 8g .. 8g+7).
+  constexpr int kQsqRegs = FOLD ? 1 : NDT * 2;
+  u32x4 qsq_pk[kQsqRegs];
+  float* frow = feat + (wave * 32 + l32) * kFoldCols;
+  if constexpr (FOLD) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) frow[8 * g + e] = 0.0f;
+    __syncthreads();
+  }
+  float tail = 0.0f;
+#pragma unroll
+  for (int ot = 0; ot < NDT; ++ot) {
+    f32x16 acc = f32x16{};
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+      acc = T::mfma32(matrix_frag(ot, 2 * s + g), qreg[s], acc);
+    float sq[16];
+#pragma unroll
+    for (int rr = 0; rr < 16; ++rr) {
+      const float x = T::to_f(T::from_f(acc[rr]));
+      sq[rr] = T::to_f(T::from_f(x * x));
+    }
+    if constexpr (FOLD) {
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) {
+        const int c = 32 * ot + mfma_row(rr, g);
+        if (c < a.rank) frow[c] = sq[rr];
+        else tail += sq[rr];
+      }
+    } else {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+        qsq_pk[2 * ot + hh] = u32x4{pack2<T>(sq[8 * hh], sq[8 * hh + 1]),
+                                    pack2<T>(sq[8 * hh + 2], sq[8 * hh + 3]),
+                                    pack2<T>(sq[8 * hh + 4], sq[8 * hh + 5]),
+                                    pack2<T>(sq[8 * hh + 6], sq[8 * hh + 7])};
+    }
+  }
+  if constexpr (FOLD) {
+    // T = sum_{c>=r} qsq_c over both lanes of the row, split into three bf16 parts.
+    const float total = pair_sum(tail);
+    const float hi = T::to_f(T::from_f(total));
+    const float mid = T::to_f(T::from_f(total - hi));
+    const float lo = T::to_f(T::from_f((total - hi) - mid));
+    if (g == 0) {
+      frow[a.rank] = hi;
+      frow[a.rank + 1] = mid;
+      frow[a.rank + 2] = lo;
+    }
+    __syncthreads();
+    const float* f8 = frow + 8 * g;
+    qsq_pk[0] = u32x4{pack2<T>(f8[0], f8[1]), pack2<T>(f8[2], f8[3]), pack2<T>(f8[4], f8[5]),
+                      pack2<T>(f8[6], f8[7])};
+  }
+  __syncthreads();  // the full kernel's table tiles reuse the U^T staging area
+
+  const float s32 = a.scale;
+  const float ssq = (float)((double)a.scale * (double)a.scale);
+  const float half = (float)(0.5 * (double)a.scale * (double)a.scale);
+  const float thsq = (float)((double)a.theta * (double)a.theta);
+  // The gate fl(quad * s^2) <= theta^2 as one compare quad <= thq: fl(x * s^2) is monotone in
+  // x, so the quads that pass form (-inf, thq], with thq within an ulp or two of
+  // theta^2 / s^2 (found by stepping; exact for every scale, not only powers of two).
+  float thq = thsq / ssq;
+  for (int i = 0; i < 4 && thq * ssq > thsq; ++i) thq = nextafterf(thq, -INFINITY);
+  for (int i = 0; i < 4 && nextafterf(thq, INFINITY) * ssq <= thsq; ++i)
+    thq = nextafterf(thq, INFINITY);
+  // Scores in log2 units: c1 on q.kbar, c2 on the gated qsq.w term.
+  const float c1 = s32 * kLog2e, c2 = half * kLog2e;
+  const float ln_full = logf((float)kBlock);
+  const float short2 = (logf((float)(a.n_video - kBlock * (a.nb - 1))) - ln_full) * kLog2e;
+  const int last_tile = (a.nb - 1) / kCoarseSlots;
+  // Block nb - 1 sits in slot sl = mfma_row(short_reg, g) of the last tile for the lanes
+  // of half g = (sl / 4) % 2; those lanes add its log2(n / 128) in units of c1.
+  const int short_slot = (a.nb - 1) % kCoarseSlots;
+  const int short_reg = 4 * (short_slot >> 3) + (short_slot & 3);
+  const float short_lane = g == ((short_slot >> 2) & 1) ? short2 / c1 : 0.0f;
 
   // The score chains of the tile in stage `st`: s = q.kbar from the bias, quad = qsq.w.
   // MFMA i of the chain: 0 the bias; folded, 1 the quad and 2 .. NS+1 the q.kbar slices;
@@ -409,11 +441,20 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
   // vbar, that of t_{i-1}, was read in step i-1).  Past the last tile the scores computed
   // are of stale LDS contents and unused.  Returns t_{i+2}.
   f32x16 sacc, wacc;
+  // The folded kernel requests C_vk in the first step, after its barrier (every wave is done
+  // with U^T), so the copy lands by the next one.
+  bool cvk_staged = false;
   auto step = [&](int k, int kn, char* cur, char* nxt) {
     tile_barrier();
     const int kn2 = kn < ntiles ? next_tile(kn) : ntiles;
     if (kn2 < ntiles) copy_kw(kn2, cur);
     if (kn < ntiles) copy_v(kn, nxt);
+    if constexpr (FOLD) {
+      if (!cvk_staged) {
+        stage_matrix(a.cvk + (int64_t)bank * D * D);
+        cvk_staged = true;
+      }
+    }
     short_fix(k, sacc);
     f32x16 sn, wn;
     float p[16], part, gpart;
@@ -423,12 +464,14 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
     wacc = wn;
     return kn2;
   };
-  int k = next_tile(-1);
+  int k = k_first;
   if (k < ntiles) {
-    int kn = next_tile(k);
-    copy_kw(k, st0);
-    copy_v(k, st0);
-    if (kn < ntiles) copy_kw(kn, st1);
+    int kn = k_second;
+    if constexpr (!FOLD) {
+      copy_kw(k, st0);
+      copy_v(k, st0);
+      if (kn < ntiles) copy_kw(kn, st1);
+    }
     tile_barrier();
     {
       float p[16], part, gpart;
@@ -446,9 +489,14 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
     }
   }
 
-  // Value drift s C_vk q in the output layout: stage C_vk over the tables' LDS.
-  __syncthreads();
-  stage_matrix(a.cvk + (int64_t)bank * D * D);
+  // Value drift s C_vk q in the output layout: C_vk in its buffer (folded; staged here only
+  // when there was no tile) or staged over the tables' LDS.
+  if constexpr (FOLD) {
+    if (!cvk_staged) stage_matrix(a.cvk + (int64_t)bank * D * D);
+  } else {
+    __syncthreads();
+    stage_matrix(a.cvk + (int64_t)bank * D * D);
+  }
   staged_barrier();
 
   const float l = pair_sum(lsum);
