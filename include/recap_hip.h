@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define RECAP_ABI_VERSION 5
+#define RECAP_ABI_VERSION 6
 
 enum { RECAP_OK = 0, RECAP_EINVAL = 1, RECAP_EUNSUPPORTED = 2, RECAP_EHIP = 3 };
 enum { RECAP_F16 = 1, RECAP_BF16 = 2 };
@@ -317,6 +317,10 @@ int recap_pager_prefetch(recap_pager* pager, int64_t key, int32_t slot);
  * so far on `stream`; the key then holds a bank.
  * Replaces _stage_out and _split_out, recap/host_banks.py:132-146, 227-242. */
 int recap_pager_stage_out(recap_pager* pager, int64_t key, int32_t slot, void* stream);
+/* Order `stream` after every transfer in flight on the slot (its last write-back, a prefetch
+ * into it), for a call that writes the slot without loading it (a first refresh).  Replaces
+ * the wait for a pending write-back from the slot, recap/host_banks.py:169-173. */
+int recap_pager_acquire(recap_pager* pager, int32_t slot, void* stream);
 /* The work queued so far on `stream` is the slot's last use before it may be refilled.
  * Replaces the slot_free event, recap/host_banks.py:194-196. */
 int recap_pager_release(recap_pager* pager, int32_t slot, void* stream);

@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "librecap_hip.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 RECAP_OK, RECAP_EINVAL, RECAP_EUNSUPPORTED, RECAP_EHIP = 0, 1, 2, 3
 RECAP_F16, RECAP_BF16 = 1, 2
@@ -70,6 +70,7 @@ SIGNATURES: dict[str, tuple] = {
     "recap_pager_stage_in": (_I, [_P, _I64, ctypes.c_int32, _P]),
     "recap_pager_prefetch": (_I, [_P, _I64, ctypes.c_int32]),
     "recap_pager_stage_out": (_I, [_P, _I64, ctypes.c_int32, _P]),
+    "recap_pager_acquire": (_I, [_P, ctypes.c_int32, _P]),
     "recap_pager_release": (_I, [_P, ctypes.c_int32, _P]),
     "recap_pager_finish": (_I, [_P]),
     "recap_pager_stored": (_I, [_P, _I64]),

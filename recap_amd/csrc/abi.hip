@@ -680,6 +680,12 @@ int recap_pager_stage_out(recap_pager* pager, int64_t key, int32_t slot, void* s
   return hip_status(pager_stage_out(as_pager(pager), key, slot, as_stream(stream)), "stage_out");
 }
 
+int recap_pager_acquire(recap_pager* pager, int32_t slot, void* stream) {
+  Pager* p = as_pager(pager);
+  REQUIRE(p != nullptr && slot >= 0 && slot < pager_slots(p), "bad pager or slot");
+  return hip_status(pager_acquire(p, slot, as_stream(stream)), "acquire");
+}
+
 int recap_pager_release(recap_pager* pager, int32_t slot, void* stream) {
   Pager* p = as_pager(pager);
   REQUIRE(p != nullptr && slot >= 0 && slot < pager_slots(p), "bad pager or slot");

@@ -154,6 +154,7 @@ hipError_t pager_reserve(Pager* p, int64_t n_keys);
 hipError_t pager_stage_in(Pager* p, int64_t key, int slot, hipStream_t s);
 hipError_t pager_prefetch(Pager* p, int64_t key, int slot);
 hipError_t pager_stage_out(Pager* p, int64_t key, int slot, hipStream_t s);
+hipError_t pager_acquire(Pager* p, int slot, hipStream_t s);
 hipError_t pager_release(Pager* p, int slot, hipStream_t s);
 hipError_t pager_finish(Pager* p);
 hipError_t pager_copy_time(Pager* p, double* total_ms, int64_t* n);

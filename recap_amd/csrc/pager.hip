@@ -11,7 +11,9 @@
 //   prefetch   key -> slot on the pager's prefetch stream, after the compute stream is done
 //              with the slot (release) and the slot's last write-back has read it out;
 //   stage_out  slot -> key on the pager's write-back stream, after the work queued so far on
-//              the compute stream (the refresh that wrote the slot).
+//              the compute stream (the refresh that wrote the slot);
+//   acquire    no transfer: the compute stream waits until the slot may be written without
+//              a load (its last write-back has read it out, no prefetch is filling it).
 //
 // Events fence every reuse: per slot (released by compute, prefetched, written back) and per
 // key (host copy written, host copy being read by a prefetch).  Streams are created
@@ -260,6 +262,17 @@ hipError_t pager_stage_out(Pager* p, int64_t key, int slot, hipStream_t s) {
   sl.resident = key;
   sl.prefetched = false;
   ++p->counts[3];
+  return hipSuccess;
+}
+
+hipError_t pager_acquire(Pager* p, int slot, hipStream_t s) {
+  // The compute stream is about to write the slot without loading it (a first refresh): a
+  // prefetch still filling it and its last write-back must be done first.
+  Slot& sl = p->slots[(size_t)slot];
+  if (sl.prefetched) HIP_TRY(wait(s, sl.ready));
+  sl.prefetched = false;
+  HIP_TRY(wait(s, sl.written));
+  sl.resident = -1;
   return hipSuccess;
 }
 

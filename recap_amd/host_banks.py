@@ -149,6 +149,8 @@ class HostBankOperator(Operator):
         if load:
             self._pager("stage_in", bank_key, slot, compute)
             self._prefetch_after(layer_index)
+        else:
+            self._pager("acquire", slot, compute)
         slot_tensors = self._slots[slot]
         nb = slot_tensors["partition"].shape[-1]
         views = dict(slot_tensors, partition=slot_tensors["partition"].view(b, h, nb, nb))
