@@ -124,6 +124,8 @@ __device__ inline void store_rows(const AttnArgs& a, int bank, int b, int h, int
     const float wh = expf(lse - common);
     const float wt = expf(tl - common);
     const float den2 = fmaxf(wh + wt, 1.0e-30f);
+    // One reciprocal per denominator and row instead of a division per element.
+    const float rden = 1.0f / den, rden2 = 1.0f / den2;
     const uint16_t* gorow = a.go + ri * D;
     const uint16_t* drow = a.det + ri * D;
 #pragma unroll
@@ -142,8 +144,8 @@ __device__ inline void store_rows(const AttnArgs& a, int bank, int b, int h, int
           const float gov = T::to_f((uint16_t)((e & 1) ? gword >> 16 : gword & 0xffff));
           const float detv = f16_to_f((uint16_t)((e & 1) ? dword >> 16 : dword & 0xffff));
           const float ohv = T::to_f((uint16_t)((e & 1) ? hword >> 16 : hword & 0xffff));
-          const float to = (gov * sm + (gov + detv) * cm) / den;
-          res[e] = (ohv * wh + to * wt) / den2;
+          const float to = (gov * sm + (gov + detv) * cm) * rden;
+          res[e] = (ohv * wh + to * wt) * rden2;
         }
         u32x2 v = {pack2<T>(res[0], res[1]), pack2<T>(res[2], res[3])};
         *reinterpret_cast<u32x2*>(orow + d0) = v;
@@ -401,10 +403,9 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
   // packed for the PV MFMAs); while PV_it runs, the row max over pairs of S_{it+1} scores.
   // The matrix core then works while the VALU does, instead of one after the other.
   // `it` is even at every call with parity tag 0 and odd with tag 1.
-  auto step = [&](int it, f32x16 (&cur)[kGroups][2], f32x16 (&nxt)[kGroups][2], auto mask_tag,
+  auto step = [&](int it, f32x16 (&cur)[kGroups][2], f32x16 (&nxt)[kGroups][2], bool mask,
                   auto next_tag, auto parity_tag) __attribute__((always_inline)) {
     constexpr bool kNext = decltype(next_tag)::value;
-    constexpr bool kMask = decltype(mask_tag)::value;
     constexpr bool kOdd = decltype(parity_tag)::value;
     if (it + 1 < nsub) copy(vrs, image(it + 1), kOdd ? v_lds0 : v_lds1);
     if (it + 2 < nsub) copy(krs, image(it + 2), kOdd ? k_lds1 : k_lds0);
@@ -421,8 +422,6 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
       const int i = n - NQK;
       return lds_load16(vl, G::vt_off(32 * (i % NDT) + l32, 2 * (i / NDT) + g));
     };
-    int limit = 64;
-    if constexpr (kMask) limit = a.n_tokens - ((a.tb - 1) * kBlock + 64 * ((it + 1) & 1));
     unsigned w[kGroups][2][2][4];
     float part[kGroups][2];
     float mx[kGroups];
@@ -452,6 +451,12 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
 #pragma unroll
         for (int q = 0; q < kGroups; ++q)
           nxt[q][kt] = T::mfma32(fr[n % 3], qreg[q][st], st == 0 ? f32x16{} : nxt[q][kt]);
+        // S_{it+1} in the ragged last block: keys past the sequence end get -inf before the
+        // row max reads them (a rare uniform branch, outside the scheduled slices).
+        if (n == NQK - 1 && mask) {
+          __builtin_amdgcn_sched_barrier(0);
+          mask_tail(nxt, it + 1);
+        }
       } else {
         const int i = n - NQK, kt = i / (2 * NDT), hh = (i / NDT) & 1, dt = i % NDT;
 #pragma unroll
@@ -464,14 +469,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
 #pragma unroll
           for (int mp = i * MPS; mp < (i + 1) * MPS; ++mp) {
             const int q = mp % kGroups, j = 2 * (mp / kGroups), kt2 = j >> 4, rr = j & 15;
-            float s0 = nxt[q][kt2][rr], s1 = nxt[q][kt2][rr + 1];
-            if constexpr (kMask) {
-              if (32 * kt2 + mfma_row(rr, g) >= limit) s0 = -INFINITY;
-              if (32 * kt2 + mfma_row(rr + 1, g) >= limit) s1 = -INFINITY;
-              nxt[q][kt2][rr] = s0;
-              nxt[q][kt2][rr + 1] = s1;
-            }
-            mx[q] = fmaxf(fmaxf(mx[q], s0), s1);  // one v_max3_f32 per pair
+            mx[q] = fmaxf(fmaxf(mx[q], nxt[q][kt2][rr]), nxt[q][kt2][rr + 1]);  // one v_max3_f32
           }
         }
       }
@@ -513,24 +511,23 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
   int it = 0;
   if constexpr (MODE != kModeDense) {
     if (nsub >= 4) {
-      if (ragged_at(1)) step(0, sa, sb, Tr{}, Tr{}, F{}); else step(0, sa, sb, F{}, Tr{}, F{});
-      if (ragged_at(2)) step(1, sb, sa, Tr{}, Tr{}, Tr{}); else step(1, sb, sa, F{}, Tr{}, Tr{});
+      step(0, sa, sb, ragged_at(1), Tr{}, F{});
+      step(1, sb, sa, ragged_at(2), Tr{}, Tr{});
       it = 2;
     }
   }
   for (; it + 4 < nsub; it += 2) {
-    step(it, sa, sb, F{}, Tr{}, F{});
-    step(it + 1, sb, sa, F{}, Tr{}, Tr{});
+    step(it, sa, sb, false, Tr{}, F{});
+    step(it + 1, sb, sa, false, Tr{}, Tr{});
   }
   if (nsub - it >= 4) {
-    step(it, sa, sb, F{}, Tr{}, F{});
-    if (ragged_at(it + 2)) step(it + 1, sb, sa, Tr{}, Tr{}, Tr{});
-    else step(it + 1, sb, sa, F{}, Tr{}, Tr{});
+    step(it, sa, sb, false, Tr{}, F{});
+    step(it + 1, sb, sa, ragged_at(it + 2), Tr{}, Tr{});
     it += 2;
   }
   if (nsub >= 2) {
-    if (ragged_at(it + 1)) step(it, sa, sb, Tr{}, Tr{}, F{}); else step(it, sa, sb, F{}, Tr{}, F{});
-    step(it + 1, sb, sa, F{}, F{}, Tr{});
+    step(it, sa, sb, ragged_at(it + 1), Tr{}, F{});
+    step(it + 1, sb, sa, false, F{}, Tr{});
   }
 
   constexpr int kStore = MODE == kModeDenseHead ? kModeDense : MODE;
