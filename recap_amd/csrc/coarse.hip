@@ -11,12 +11,15 @@
 // host-side planning or synchronisation is needed (recap/sparse/planner.py:24-27 is the
 // host sync this removes).
 //
-// One workgroup = one (bank, 128-row query block), 4 waves x 32 rows.  The three
-// contractions per 32-block tile (q.kbar, qsq.w, p.vbar) run on 32x32x16 MFMA with the
-// same register-resident layout trick as the attention kernel: the fp32 result of one
-// MFMA is the B operand of the next, and the tables' columns (w) or rows (vbar^T) are
-// stored in the matching swap23 order, as tile images copied verbatim into LDS.  Also writes per-block partial sums of
-// (gl - gl_ref) for the per-bank drift centre (recap/operator.py:148-150).
+// One workgroup = one (bank, 128-row query block), 4 waves x 32 rows.  The contractions
+// per 32-block tile (q.kbar, qsq.w, p.vbar, and one MFMA that puts -inf on the kept blocks'
+// scores) run on 32x32x16 MFMA with the same register-resident layout trick as the
+// attention kernel: the fp32 result of one MFMA is the B operand of the next, and the
+// tables' columns (w) or rows (vbar^T) are stored in the matching swap23 order, as tile
+// images copied verbatim into LDS.  The tile loop is pipelined: a tile's score chains run
+// on the matrix cores while the previous tile's softmax runs on the VALU.  Also writes
+// per-block partial sums of (gl - gl_ref) for the per-bank drift centre
+// (recap/operator.py:148-150).
 #include "kernels.hpp"
 
 namespace recap {
