@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define RECAP_ABI_VERSION 6
+#define RECAP_ABI_VERSION 7
 
 enum { RECAP_OK = 0, RECAP_EINVAL = 1, RECAP_EUNSUPPORTED = 2, RECAP_EHIP = 3 };
 enum { RECAP_F16 = 1, RECAP_BF16 = 2 };
@@ -132,13 +132,12 @@ int recap_symmetric_eigen(const float* a, int64_t batch, int64_t n, float* eigen
                           float* eigenvectors, void* stream);
 
 /* Query-type tables of the coarse tail: w = fold_rank(variance, rank), kbar, vbar, each
- * written as tile images of 32 key blocks, [banks, ceil(nb/32)*32, width] elements (rows
- * past nb zero), width = dim for kbar and vbar and recap_coarse_w_width() for w.  kbar
- * tiles are in the packed K-tile layout, vbar tiles transposed ([dim][32 positions],
- * position p holding block swap23(p)), so the coarse tail copies a tile verbatim into LDS.
- * w is either the full fold_rank row in the K-tile layout (columns in swap23 order) or,
- * when the fold leaves few distinct values (bf16, 1 <= rank <= 13), the 16 features
- * [w_0 .. w_{rank-1}, rho, rho, rho, 0 ...] with rho the mean of the folded columns.
+ * [banks, ceil(nb/32)*32, width] elements, row j holding key block j (rows past nb zero),
+ * width = dim for kbar and vbar and recap_coarse_w_width() for w.  The coarse tail gathers
+ * the rows of the blocks it visits from these tables.  w is either the full fold_rank row
+ * (columns in swap23 order) or, when the fold leaves few distinct values (bf16,
+ * 1 <= rank <= 13), the 16 features [w_0 .. w_{rank-1}, rho, rho, rho, 0 ...] with rho the
+ * mean of the folded columns.
  * Replaces fold_rank (recap/sparse/closure.py:96-104) and the casts of
  * recap/kernels/coarse_tail.py:238-241. */
 int recap_coarse_tables(const float* variance, const float* k_means, const float* v_means,
@@ -160,7 +159,7 @@ int recap_basis_tables(const float* basis, const float* cvk, int dtype, int64_t 
 
 /* Corrected coarse tail for the R refined rows: go [banks, R, dim] (query type),
  * gl [banks, R] fp32; with glref [banks, R] also drift_partial [banks, R/128].  kbar, vbar
- * and w are the tile images written by recap_coarse_tables with the same dtype, dim and
+ * and w are the tables written by recap_coarse_tables with the same dtype, dim and
  * rank (the closure rank of fold_rank, which selects the w layout).
  * Replaces coarse_tail_attention + _coarse_tail_kernel (recap/kernels/coarse_tail.py:
  * 35-312), build_coarse_tail_plan (recap/sparse/planner.py:11-38), rotated_query_square

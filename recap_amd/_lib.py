@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "librecap_hip.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 RECAP_OK, RECAP_EINVAL, RECAP_EUNSUPPORTED, RECAP_EHIP = 0, 1, 2, 3
 RECAP_F16, RECAP_BF16 = 1, 2

@@ -331,18 +331,16 @@ hipError_t run_partial_reduce(const float* part, int banks, int groups, int elem
 
 // One workgroup per padded table row (bank, j), j < ntiles * 32: fold_rank of the rotated
 // variance (recap/sparse/closure.py:96-104), then w, kbar, vbar rounded to the query type
-// and written into their tile images (rows j >= nb are zero).  FOLD writes w as the
-// kFoldCols-feature row [w_0 .. w_{r-1}, rho, rho, rho, 0 ...] (natural order), 32 rows of
-// 32 bytes per tile.
+// and written as row j of their tables, plain row-major D-element rows (rows j >= nb are
+// zero); the non-folded w row holds its columns in swap23 order.  FOLD writes w as the
+// kFoldCols-feature row [w_0 .. w_{r-1}, rho, rho, rho, 0 ...] (natural order), 32 bytes.
 template <class T, int D, bool FOLD>
 __global__ __launch_bounds__(128) void tables_kernel(TablesArgs a) {
-  using G = TileGeom<D>;
   __shared__ float red[128];
   __shared__ float vals[128];
   const int ntiles = (a.nb + kCoarseSlots - 1) / kCoarseSlots;
   const int bank = blockIdx.x / (ntiles * kCoarseSlots);
   const int j = blockIdx.x % (ntiles * kCoarseSlots);
-  const int tile = j / kCoarseSlots, slot = j % kCoarseSlots;
   const bool real = j < a.nb;
   const int64_t row = (int64_t)bank * a.nb + j;
   const int t = threadIdx.x;
@@ -358,10 +356,10 @@ __global__ __launch_bounds__(128) void tables_kernel(TablesArgs a) {
   vals[t] = (fold && t >= a.rank) ? residual : v;
   __syncthreads();
   if (t < D) {
-    const int64_t tile_base = ((int64_t)bank * ntiles + tile) * kCoarseSlots * D * 2;  // bytes
-    const int koff = G::k_off(slot, t >> 3) + ((t & 7) << 1);
-    const uint16_t kv = real ? T::from_f(a.kmean[row * D + t]) : (uint16_t)0;
-    const uint16_t vv = real ? T::from_f(a.vmean[row * D + t]) : (uint16_t)0;
+    // Row j of the bank's tables: element t of block j (zeros past the last block).
+    const int64_t at = ((int64_t)bank * ntiles * kCoarseSlots + j) * D + t;
+    a.kbar_t[at] = real ? T::from_f(a.kmean[row * D + t]) : (uint16_t)0;
+    a.vbar_t[at] = real ? T::from_f(a.vmean[row * D + t]) : (uint16_t)0;
     if constexpr (FOLD) {
       if (t < kFoldCols) {
         const float f = t < a.rank ? vals[t] : (t < a.rank + 3 ? residual : 0.0f);
@@ -369,12 +367,8 @@ __global__ __launch_bounds__(128) void tables_kernel(TablesArgs a) {
             real ? T::from_f(f) : (uint16_t)0;
       }
     } else {
-      const uint16_t wv = real ? T::from_f(vals[swap23(t)]) : (uint16_t)0;
-      *reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(a.w_t) + tile_base + koff) = wv;
+      a.w_t[at] = real ? T::from_f(vals[swap23(t)]) : (uint16_t)0;  // columns in swap23 order
     }
-    *reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(a.kbar_t) + tile_base + koff) = kv;
-    *reinterpret_cast<uint16_t*>(reinterpret_cast<char*>(a.vbar_t) + tile_base +
-                                 coarse_vt_off(t, swap23(slot))) = vv;
   }
 }
 

@@ -6,20 +6,20 @@
 //   drift = s C_vk q       in the query type  (recap/sparse/closure.py:89-93)
 //   l_j   = s q.kbar_j + ln n_j + [s^2 qsq.w_j <= theta^2] (s^2/2) qsq.w_j
 //   out   = softmax(l) . vbar  (+ g * drift, g = gated share of the mass), lse = m + ln l
-// over the omitted blocks j (~partition[i, j]), walked in 32-block tiles of the tables with
-// the partition row as a bit mask (tiles without an omitted block are skipped), so no
-// host-side planning or synchronisation is needed (recap/sparse/planner.py:24-27 is the
-// host sync this removes).
+// over the omitted blocks j (~partition[i, j]).  Each workgroup first compacts its
+// partition row into the ascending list of its omitted blocks (a ballot count per wave and
+// chunk, one scan), then walks that list in tiles of 32 blocks gathered from the tables, so
+// only omitted blocks are computed and no host-side planning or synchronisation is needed
+// (recap/sparse/planner.py:24-27 is the host sync this removes).
 //
 // One workgroup = one (bank, 128-row query block), 4 waves x 32 rows.  The contractions
-// per 32-block tile (q.kbar, qsq.w, p.vbar, and one MFMA that puts -inf on the kept blocks'
-// scores) run on 32x32x16 MFMA with the same register-resident layout trick as the
-// attention kernel: the fp32 result of one MFMA is the B operand of the next, and the
-// tables' columns (w) or rows (vbar^T) are stored in the matching swap23 order, as tile
-// images copied verbatim into LDS.  The tile loop is pipelined: a tile's score chains run
-// on the matrix cores while the previous tile's softmax runs on the VALU.  Also writes
-// per-block partial sums of (gl - gl_ref) for the per-bank drift centre
-// (recap/operator.py:148-150).
+// per 32-block tile (q.kbar, qsq.w, p.vbar, and one MFMA that puts -inf on the padding
+// slots' scores) run on 32x32x16 MFMA with the same register-resident layout trick as the
+// attention kernel: the fp32 result of one MFMA is the B operand of the next, the w table's
+// columns are stored in the matching swap23 order, and vbar is read slot-major through the
+// transposing LDS read.  The tile loop is pipelined: a tile's score chains run on the
+// matrix cores while the previous tile's softmax runs on the VALU.  Also writes per-block
+// partial sums of (gl - gl_ref) for the per-bank drift centre (recap/operator.py:148-150).
 #include "kernels.hpp"
 
 namespace recap {
@@ -37,19 +37,20 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
   constexpr int kWBytes = FOLD ? kCoarseSlots * kFoldCols * 2 : kTabBytes;
   constexpr int kStage = 2 * kTabBytes + kWBytes;  // kbar, vbar, w of one tile
   constexpr int NDMA = kTabBytes / 4096;           // 16-byte copies per thread per image
-  static_assert(FOLD || 2 * kStage >= kMatBytes, "a staged D x D matrix spans both stages");
+  constexpr int kScan = kMaxVideoBlocks / 256;     // chunks of the partition row
+  static_assert(2 * kStage >= kMatBytes, "a staged D x D matrix spans both stages");
   static_assert(!FOLD || kWBytes == 1024, "a folded w tile is 4 bytes per thread");
+  static_assert(4 * kScan <= 64, "the chunk counts are scanned by one wave");
   // Two tile stages in separate arrays, each access naming one of them at compile time: the
   // compiler can then tell that reads of one stage do not touch the copies filling the other,
   // and does not wait for those copies first.  A staged D x D matrix (U^T, C_vk) keeps rows
-  // 0 .. D/2-1 and the rest in two halves of the same swizzled layout (it depends on the row's
-  // low bits only): in the folded kernel in a buffer of its own (43.5 + 32 KB, still two
-  // workgroups per CU), so the first tiles arrive while qsq runs and C_vk while the tiles
-  // do; in the full one, whose stages are larger, over stages 0 and 1.
+  // 0 .. D/2-1 in stage 0 and the rest in stage 1 (same swizzle: it depends on the row's low
+  // bits only).
   __shared__ __attribute__((aligned(16))) char st0[kStage];
   __shared__ __attribute__((aligned(16))) char st1[kStage];
-  __shared__ __attribute__((aligned(16))) char mat[FOLD ? kMatBytes : 16];
-  __shared__ unsigned omit[kMaxVideoBlocks / kCoarseSlots];
+  // This query block's omitted blocks, ascending, then zeros up to the next multiple of 32.
+  __shared__ uint16_t olist[kMaxVideoBlocks + kCoarseSlots];
+  __shared__ int counts[4 * kScan + 1];
   __shared__ float wsum[4];
   __shared__ float feat[FOLD ? 4 * 32 * kFoldCols : 1];  // folded qsq features per row
 
@@ -58,7 +59,7 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
   const int lin = xcd_linear(blockIdx.x, a.banks * a.qtiles);
   const int bank = lin / a.qtiles, qt = lin % a.qtiles;
   const int b = bank / a.heads, h = bank % a.heads;
-  const int ntiles = (a.nb + kCoarseSlots - 1) / kCoarseSlots;
+  const int ntiles = (a.nb + kCoarseSlots - 1) / kCoarseSlots;  // table rows / 32
 
   // Stage a D x D matrix of the query type (row-major in HBM) into LDS by buffer loads into
   // LDS, all in flight at once: one wave instruction fills 1 KB of the swizzled image in lane
@@ -73,11 +74,9 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
       const int pos = 4096 * i + 16 * t;  // byte position in the half image
       const int row = pos / (2 * D), pc = (pos % (2 * D)) >> 4;
       const int from = row * 2 * D + ((pc ^ G::swz(row, NCH)) << 4);
-      char* lo = FOLD ? mat : st0;
-      char* hi = FOLD ? mat + kHalfBytes : st1;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(lo + 4096 * i + 1024 * wave), 16,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(st0 + 4096 * i + 1024 * wave), 16,
                                                from, 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(hi + 4096 * i + 1024 * wave), 16,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(st1 + 4096 * i + 1024 * wave), 16,
                                                from + kHalfBytes, 0, 0, 0);
     }
   };
@@ -90,12 +89,8 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
   };
   // Fragment of row tile `rt` (32 rows) of a staged matrix; rt is a compile-time index.
   auto matrix_frag = [&](int rt, int chunk) {
-    if constexpr (FOLD)
-      return rt < NDT / 2 ? lds_load16(mat, G::k_off(32 * rt + l32, chunk))
-                          : lds_load16(mat + kMatBytes / 2, G::k_off(32 * (rt - NDT / 2) + l32, chunk));
-    else
-      return rt < NDT / 2 ? lds_load16(st0, G::k_off(32 * rt + l32, chunk))
-                          : lds_load16(st1, G::k_off(32 * (rt - NDT / 2) + l32, chunk));
+    return rt < NDT / 2 ? lds_load16(st0, G::k_off(32 * rt + l32, chunk))
+                        : lds_load16(st1, G::k_off(32 * (rt - NDT / 2) + l32, chunk));
   };
   // U^T and this wave's row-map entry are requested before the partition row, so all three
   // arrive in one wait.
@@ -103,13 +98,16 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
   const int r = qt * kBlock + wave * 32 + l32;  // always < rows
   const int nat = a.rowmap[r];
 
-  // Omitted blocks of this query block (partition 0) as one bit word per table tile.  All
-  // of the row's loads are issued before the first ballot, so the scan waits once, and the
-  // Q row (which waits only for the row-map entry) is requested in between.
+  // The omitted blocks of this query block (partition 0), compacted in ascending order into
+  // olist: block j's place is the number of omitted blocks before it, i.e. the counts of the
+  // earlier (chunk of 256, wave) pairs, scanned by one wave, plus the omitted lanes below it
+  // in its ballot.  All of the row's loads are issued before the first ballot, and the Q
+  // row (which waits only for the row-map entry) in between.
   u32x4 qreg[NS];
+  int n_om;
   {
     const uint8_t* prow = a.partition + ((int64_t)bank * a.nb + qt) * a.nb;
-    constexpr int kScan = kMaxVideoBlocks / 256;
+    const int nchunks = (a.nb + 255) / 256;
     uint8_t cell[kScan];
 #pragma unroll
     for (int i = 0; i < kScan; ++i) cell[i] = prow[min(256 * i + t, a.nb - 1)];  // in the row
@@ -122,23 +120,50 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
       if (256 * i + t < a.nb && cell[i] == 0) flags |= 1u << i;
 #pragma unroll
     for (int i = 0; i < kScan; ++i) {
-      if (256 * i >= ntiles * kCoarseSlots) break;
-      const unsigned long long bal = __ballot((flags >> i) & 1u);
-      const int wi = (256 * i + 64 * wave) / kCoarseSlots;
-      if (lane == 0 && wi < ntiles) omit[wi] = (unsigned)bal;
-      if (lane == 0 && wi + 1 < ntiles) omit[wi + 1] = (unsigned)(bal >> 32);
+      if (i < nchunks) {  // uniform
+        const unsigned long long bal = __ballot((flags >> i) & 1u);
+        if (lane == 0) counts[4 * i + wave] = (int)__popcll(bal);
+      }
     }
+    __syncthreads();
+    if (wave == 0) {  // exclusive prefix of the 4 * nchunks counts, the total after them
+      const int n = 4 * nchunks;
+      const int own = lane < n ? counts[lane] : 0;
+      int v = own;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int u = __shfl_up(v, off, 64);
+        if (lane >= off) v += u;
+      }
+      if (lane < n) counts[lane] = v - own;
+      if (lane == 63) counts[4 * kScan] = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kScan; ++i) {
+      if (i < nchunks) {  // uniform
+        const unsigned long long bal = __ballot((flags >> i) & 1u);
+        if ((flags >> i) & 1u)
+          olist[counts[4 * i + wave] + (int)__popcll(bal & ((1ull << lane) - 1ull))] =
+              (uint16_t)(256 * i + t);
+      }
+    }
+    n_om = __builtin_amdgcn_readfirstlane(counts[4 * kScan]);
+    if (t < kCoarseSlots) olist[n_om + t] = 0;  // padding slots read table row 0
   }
 
   staged_barrier();
 
-  // Table tiles (images written by the tables kernel) are copied verbatim into LDS by
-  // buffer loads over this bank's images; tiles with no omitted block are skipped.  The
-  // loop is pipelined across tiles: while the softmax and p.vbar of tile t_i run, the
-  // q.kbar and qsq.w chains of t_{i+1} run on the matrix cores, so a wave's MFMAs overlap
-  // its own VALU work.  Tile t_i lives in stage i % 2 (layout: kbar, vbar, w images); its
-  // kbar and w images arrive two tiles ahead (they are read one tile ahead), its vbar image
-  // one tile ahead.
+  // Tiles of 32 omitted blocks (the last one padded), gathered into LDS by buffer loads from
+  // the tables (rows of the query type, one per key block): each lane copies the 16-byte
+  // chunk its LDS position holds, K-tile layout with the compacted slot as the row, so kbar,
+  // vbar and w images read exactly like packed tiles.  Padding slots read table row 0 and
+  // are masked.  The loop is pipelined across tiles: while the softmax and p.vbar of tile
+  // i run, the q.kbar and qsq.w chains of tile i+1 run on the matrix cores, so a wave's
+  // MFMAs overlap its own VALU work.  Tile i lives in stage i % 2 (layout: kbar, vbar, w
+  // images); its kbar and w images arrive two tiles ahead (they are read one tile ahead), its
+  // vbar image one tile ahead.
+  const int ntc = (n_om + kCoarseSlots - 1) / kCoarseSlots;
   const int bank_tab = ntiles * kTabBytes;
   const int64_t tab_elems = (int64_t)bank * ntiles * kCoarseSlots * D;
   const int64_t w_elems = (int64_t)bank * ntiles * (kWBytes / 2);
@@ -148,27 +173,33 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
       (void*)(a.w + w_elems), 0, ntiles * kWBytes, kBufferRsrcWord3);
   const __amdgpu_buffer_rsrc_t vrs =
       __builtin_amdgcn_make_buffer_rsrc((void*)(a.vbar + tab_elems), 0, bank_tab, kBufferRsrcWord3);
-  auto copy_kw = [&](int k, char* dst) {  // kbar and w images of tile k
-    const int off = __builtin_amdgcn_readfirstlane(k * kTabBytes);
+  auto slot_block = [&](int c, int s) {  // table row of compacted slot s of tile c
+    return (int)olist[kCoarseSlots * c + s];
+  };
+  // Byte offset in a D-wide table of the chunk at LDS position `pos` of a tile image.
+  auto gather_src = [&](int c, int pos) {
+    const int row = pos / (2 * D), pc = (pos % (2 * D)) >> 4;
+    return slot_block(c, row) * 2 * D + ((pc ^ G::swz(row, NCH)) << 4);
+  };
+  auto copy_kw = [&](int c, char* dst) {  // kbar and w images of tile c
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) {
-      const int lo = 4096 * i + 1024 * wave, vo = 4096 * i + 16 * t;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void*)(dst + lo), 16, vo, off, 0, 0);
+      const int lo = 4096 * i + 1024 * wave, src = gather_src(c, 4096 * i + 16 * t);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void*)(dst + lo), 16, src, 0, 0, 0);
       if constexpr (!FOLD)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_void*)(dst + 2 * kTabBytes + lo), 16, vo, off, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_void*)(dst + 2 * kTabBytes + lo), 16, src, 0, 0, 0);
     }
-    if constexpr (FOLD) {  // 1 KB: 4 bytes per thread
-      const int woff = __builtin_amdgcn_readfirstlane(k * kWBytes);
+    if constexpr (FOLD) {  // 1 KB: 4 bytes per thread, row t / 8 of 32-byte rows
+      const int src = slot_block(c, t >> 3) * (kWBytes / kCoarseSlots) + 4 * (t & 7);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_void*)(dst + 2 * kTabBytes + 256 * wave), 4,
-                                               4 * t, woff, 0, 0);
+                                               src, 0, 0, 0);
     }
   };
-  auto copy_v = [&](int k, char* dst) {  // vbar image of tile k
-    const int off = __builtin_amdgcn_readfirstlane(k * kTabBytes);
+  auto copy_v = [&](int c, char* dst) {  // vbar image of tile c
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) {
-      const int lo = 4096 * i + 1024 * wave, vo = 4096 * i + 16 * t;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void*)(dst + kTabBytes + lo), 16, vo, off, 0, 0);
+      const int lo = 4096 * i + 1024 * wave, src = gather_src(c, 4096 * i + 16 * t);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void*)(dst + kTabBytes + lo), 16, src, 0, 0, 0);
     }
   };
   // This wave's copies into LDS have landed and every wave has passed the same point.
@@ -179,49 +210,17 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
     asm volatile("" ::: "memory");
   };
   // Operands of the bias MFMA that starts each tile's q.kbar accumulator: A[slot][0] = -inf
-  // for a kept slot, 0 for an omitted one; B[0][row] = 1; every other element of A and B is
-  // 0, so no -inf meets a 0.  The product is -inf on the kept slots and +0 on the omitted
-  // ones, where the chain then runs exactly as from a zero accumulator; a kept slot stays
-  // -inf through the chain and gets p = exp2(-inf) = 0 with no per-score select.
+  // for a padding slot, 0 for a block; B[0][row] = 1; every other element of A and B is 0,
+  // so no -inf meets a 0.  The product is -inf on the padding slots and +0 on the others,
+  // where the chain then runs exactly as from a zero accumulator; a padding slot stays -inf
+  // through the chain and gets p = exp2(-inf) = 0 with no per-score select.
   const unsigned bias_kept = g == 0 ? pack2<T>(-INFINITY, 0.0f) : 0u;
   const u32x4 bias_ones = u32x4{g == 0 ? pack2<T>(1.0f, 0.0f) : 0u, 0u, 0u, 0u};
-  // The omitted-block words in registers (lane i of ow_lo / ow_hi holds the word of tile i /
-  // 64 + i) and the tiles that have one as bit masks on the scalar unit, so the walk reads
-  // no LDS for its bookkeeping.
-  const unsigned ow_lo = lane < ntiles ? omit[lane] : 0u;
-  const unsigned ow_hi = 64 + lane < ntiles ? omit[64 + lane] : 0u;
-  const unsigned long long ne_lo = __ballot(ow_lo != 0), ne_hi = __ballot(ow_hi != 0);
-  auto next_tile = [&](int k) {  // the first tile after k with an omitted block, or ntiles
-    ++k;
-    if (k < 64) {
-      const unsigned long long m = ne_lo >> k;
-      if (m) return k + (int)__builtin_ctzll(m);
-      k = 64;
-    }
-    if (k < 128) {
-      const unsigned long long m = ne_hi >> (k - 64);
-      if (m) return k + (int)__builtin_ctzll(m);
-    }
-    return ntiles;
+  // Slots of tile c that hold a block (bit s), 0 past the last tile.
+  auto omit_word = [&](int c) -> unsigned {
+    const int left = n_om - kCoarseSlots * c;
+    return left >= kCoarseSlots ? ~0u : (left > 0 ? (1u << left) - 1u : 0u);
   };
-  // Omitted-block word of tile k (0 past the last tile).
-  auto omit_word = [&](int k) -> unsigned {
-    if (k >= ntiles) return 0u;
-    return k < 64 ? (unsigned)__builtin_amdgcn_readlane((int)ow_lo, k)
-                  : (unsigned)__builtin_amdgcn_readlane((int)ow_hi, k - 64);
-  };
-
-  // The first two tiles with an omitted block; the folded kernel copies their images now,
-  // while the qsq MFMAs run (both stages are free: U^T is in its own buffer).
-  const int k_first = next_tile(-1);
-  const int k_second = k_first < ntiles ? next_tile(k_first) : ntiles;
-  if constexpr (FOLD) {
-    if (k_first < ntiles) {
-      copy_kw(k_first, st0);
-      copy_v(k_first, st0);
-      if (k_second < ntiles) copy_kw(k_second, st1);
-    }
-  }
 
   // qsq = (U^T q)^2 in the query type (rotated value rounded, then its square rounded):
   // lane (g, l32) holds dims 32 ot + mfma_row(rr, g) of its row.  Full form: qsq in the
@@ -281,7 +280,7 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
     qsq_pk[0] = u32x4{pack2<T>(f8[0], f8[1]), pack2<T>(f8[2], f8[3]), pack2<T>(f8[4], f8[5]),
                       pack2<T>(f8[6], f8[7])};
   }
-  __syncthreads();  // the full kernel's table tiles reuse the U^T staging area
+  __syncthreads();  // the table tiles reuse the U^T staging area
 
   const float s32 = a.scale;
   const float ssq = (float)((double)a.scale * (double)a.scale);
@@ -298,10 +297,12 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
   const float c1 = s32 * kLog2e, c2 = half * kLog2e;
   const float ln_full = logf((float)kBlock);
   const float short2 = (logf((float)(a.n_video - kBlock * (a.nb - 1))) - ln_full) * kLog2e;
-  const int last_tile = (a.nb - 1) / kCoarseSlots;
-  // Block nb - 1 sits in slot sl = mfma_row(short_reg, g) of the last tile for the lanes
-  // of half g = (sl / 4) % 2; those lanes add its log2(n / 128) in units of c1.
-  const int short_slot = (a.nb - 1) % kCoarseSlots;
+  // Block nb - 1, when omitted, is the last of the list: slot sl of tile short_tile, held by
+  // register short_reg of the lanes of half g = (sl / 4) % 2 (sl = mfma_row(short_reg, g)),
+  // which add its log2(n / 128) in units of c1.
+  const bool short_omitted = n_om > 0 && olist[n_om - 1] == a.nb - 1;
+  const int short_tile = short_omitted && short2 != 0.0f ? (n_om - 1) / kCoarseSlots : -1;
+  const int short_slot = (n_om - 1) % kCoarseSlots;
   const int short_reg = 4 * (short_slot >> 3) + (short_slot & 3);
   const float short_lane = g == ((short_slot >> 2) & 1) ? short2 / c1 : 0.0f;
 
@@ -328,6 +329,43 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
       else sacc = T::mfma32(f, qreg[(i - 1) >> 1], sacc);
     }
   };
+  // A operand of the p.vbar MFMA (output tile dt, slot half hh): rows 32 dt + l32 (value
+  // dimensions) by slots in the order of the probabilities' packing, k = 8 g + e holding
+  // slot 16 hh + 8 (e / 4) + 4 g + e % 4.  The vbar image has the slots as rows, so two
+  // transposing reads (ds_read_b64_tr_b16: in each group of 16 lanes, lanes 4 r .. 4 r + 3
+  // supply row r of a 4 x 16 block, four 16-bit elements each, and lane i receives its
+  // column i) give each lane its four consecutive slots of one dimension, twice.
+  // Lane (grp = lane / 16, i = lane % 16, rq = i / 4, q = i % 4) reads row 16 hh + 8 e4 + 4 g
+  // + rq at dimensions d .. d+3, d = 32 dt + 16 (grp % 2) + 4 q: chunk c = d / 8 of the row,
+  // stored at c ^ swz(row).  At D = 128, swz(row) = row % 16, and bits 0-1 of c ^ swz
+  // depend on the lane only, while bits 2-3 are x ^ g with x = dt ^ 2 e4 known at compile
+  // time: x + g for even x, x - g for odd x.  Two per-lane bases then serve every read, the
+  // rest being the instruction's immediate offset.
+  const int vgrp = lane >> 4, vrq = (lane >> 2) & 3, vq = lane & 3;
+  const int vlane = 256 * vrq + 16 * (((2 * (vgrp & 1) + (vq >> 1)) ^ vrq) & 3) + 8 * (vq & 1) +
+                    1024 * g;
+  const int vb_even = vlane + 64 * g, vb_odd = vlane - 64 * g;
+  auto vbar_off = [&](int dt, int hh, int e4) {
+    if constexpr (D == 128) {
+      const int x = dt ^ (2 * e4);
+      return (x & 1 ? vb_odd : vb_even) + 4096 * hh + 2048 * e4 + 64 * x;
+    } else {
+      const int row = 16 * hh + 8 * e4 + 4 * g + vrq;
+      const int d = 32 * dt + 16 * (vgrp & 1) + 4 * vq;
+      return row * 2 * D + (((d >> 3) ^ G::swz(row, NCH)) << 4) + 8 * ((d >> 2) & 1);
+    }
+  };
+  auto vbar_frag = [&](const char* vt, int dt, int hh) {
+    u32x4 out;
+#pragma unroll
+    for (int e4 = 0; e4 < 2; ++e4) {
+      const u32x2 v = __builtin_bit_cast(
+          u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((s16x4_lds*)(vt + vbar_off(dt, hh, e4))));
+      out[2 * e4] = v[0];
+      out[2 * e4 + 1] = v[1];
+    }
+    return out;
+  };
 
   // Running max m2 (log2 units), raised lazily: a tile's probabilities are first taken
   // against the current m2, and only when a lane's sum of them exceeds kSumCap (or is not
@@ -340,12 +378,12 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) oacc[dt] = f32x16{};
 
-  // Lane (g, l32) holds slots mfma_row(rr, g); kept slots hold s = -inf.  The log-count
+  // Lane (g, l32) holds slots mfma_row(rr, g); padding slots hold s = -inf.  The log-count
   // ln 128 common to every full block is left out of the scores and added to the LSE at the
   // end (softmax, gated share and output do not depend on it); the short last block gets
   // its log2(n / 128) added to its q.kbar score (units of c1).
-  auto short_fix = [&](int k, f32x16& sacc) {
-    if (k == last_tile && short2 != 0.0f) {
+  auto short_fix = [&](int c, f32x16& sacc) {
+    if (c == short_tile) {
       int sreg = short_reg;
       asm volatile("" : "+s"(sreg));  // keeps the 16 compares in this rare branch
 #pragma unroll
@@ -364,9 +402,9 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
     gpart += gate ? p[rr] : 0.0f;
   };
 
-  // The score chains of the tile in stage `st` (omitted word ow) into sn/wn.  With a
-  // softmax to do (`probs`), the first pass of the probabilities of the current tile's
-  // scores (sacc/wacc) is spread over the chain: each MFMA is followed by one or two slots'
+  // The score chains of the tile in stage `st` (slot word ow) into sn/wn.  With a softmax
+  // to do (`probs`), the first pass of the probabilities of the current tile's scores
+  // (sacc/wacc) is spread over the chain: each MFMA is followed by one or two slots'
   // probabilities, so the wave issues them while the MFMA runs (the chain's MFMAs depend
   // on each other), and the A operands are read from LDS two MFMAs ahead.
   auto scores = [&](const char* st, unsigned ow, f32x16& sn, f32x16& wn, auto probs,
@@ -393,15 +431,15 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
     }
   };
 
-  // The rest of tile k after the first pass of its probabilities: the check of their sums
+  // The rest of a tile after the first pass of its probabilities: the check of their sums
   // (and the redo with a raised m2), the running sums and the p.vbar product (vbar image in
   // stage `st`).
   auto finish_tile = [&](const char* st, const f32x16& sacc, const f32x16& wacc, float* p,
                          float part, float gpart) {
     const char* vt_lds = st + kTabBytes;
     if (__any(!(part <= kSumCap))) {
-      // Raise m2 to the running max over this tile's omitted slots (both lanes of a row; a
-      // kept slot's score is -inf).  On the first tile, where m2 = -inf, the kept slots gave
+      // Raise m2 to the running max over this tile's slots (both lanes of a row; a padding
+      // slot's score is -inf).  On the first tile, where m2 = -inf, the padding slots gave
       // p = NaN (-inf + inf) above, which also lands here.
       float mx = -INFINITY;
 #pragma unroll
@@ -433,73 +471,47 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
-        oacc[dt] = T::mfma32(lds_load16(vt_lds, coarse_vt_off(32 * dt + l32, 8 * (2 * hh + g))),
-                             pk[hh], oacc[dt]);
+      for (int hh = 0; hh < 2; ++hh) oacc[dt] = T::mfma32(vbar_frag(vt_lds, dt, hh), pk[hh], oacc[dt]);
   };
 
-  // One step i: tile k = t_i (scores in sacc/wacc, vbar in stage `cur`) and the scores of
-  // kn = t_{i+1} (kbar/w in stage `nxt`).  Copies issued: kbar/w of t_{i+2} into `cur`
-  // (its kbar/w, those of t_i, were read in step i-1) and vbar of t_{i+1} into `nxt` (its
-  // vbar, that of t_{i-1}, was read in step i-1).  Past the last tile the scores computed
-  // are of stale LDS contents and unused.  Returns t_{i+2}.
+  // One step i: tile i (scores in sacc/wacc, vbar in stage `cur`) and the scores of tile
+  // i+1 (kbar/w in stage `nxt`).  Copies issued: kbar/w of tile i+2 into `cur` (its kbar/w,
+  // those of tile i, were read in step i-1) and vbar of tile i+1 into `nxt` (its vbar, that
+  // of tile i-1, was read in step i-1).  Past the last tile the scores computed are of stale
+  // LDS contents and unused.
   f32x16 sacc, wacc;
-  // The folded kernel requests C_vk in the first step, after its barrier (every wave is done
-  // with U^T), so the copy lands by the next one.
-  bool cvk_staged = false;
-  auto step = [&](int k, int kn, char* cur, char* nxt) {
+  auto step = [&](int c, char* cur, char* nxt) {
     tile_barrier();
-    const int kn2 = kn < ntiles ? next_tile(kn) : ntiles;
-    if (kn2 < ntiles) copy_kw(kn2, cur);
-    if (kn < ntiles) copy_v(kn, nxt);
-    if constexpr (FOLD) {
-      if (!cvk_staged) {
-        stage_matrix(a.cvk + (int64_t)bank * D * D);
-        cvk_staged = true;
-      }
-    }
-    short_fix(k, sacc);
+    if (c + 2 < ntc) copy_kw(c + 2, cur);
+    if (c + 1 < ntc) copy_v(c + 1, nxt);
+    short_fix(c, sacc);
     f32x16 sn, wn;
     float p[16], part, gpart;
-    scores(nxt, omit_word(kn), sn, wn, std::true_type{}, sacc, wacc, p, part, gpart);
+    scores(nxt, omit_word(c + 1), sn, wn, std::true_type{}, sacc, wacc, p, part, gpart);
     finish_tile(cur, sacc, wacc, p, part, gpart);
     sacc = sn;
     wacc = wn;
-    return kn2;
   };
-  int k = k_first;
-  if (k < ntiles) {
-    int kn = k_second;
-    if constexpr (!FOLD) {
-      copy_kw(k, st0);
-      copy_v(k, st0);
-      if (kn < ntiles) copy_kw(kn, st1);
-    }
+  if (ntc > 0) {
+    copy_kw(0, st0);
+    copy_v(0, st0);
+    if (ntc > 1) copy_kw(1, st1);
     tile_barrier();
     {
       float p[16], part, gpart;
-      scores(st0, omit_word(k), sacc, wacc, std::false_type{}, sacc, wacc, p, part, gpart);
+      scores(st0, omit_word(0), sacc, wacc, std::false_type{}, sacc, wacc, p, part, gpart);
     }
-    while (true) {
-      int kn2 = step(k, kn, st0, st1);
-      if (kn >= ntiles) break;
-      k = kn;
-      kn = kn2;
-      kn2 = step(k, kn, st1, st0);
-      if (kn >= ntiles) break;
-      k = kn;
-      kn = kn2;
+    for (int c = 0;; c += 2) {
+      step(c, st0, st1);
+      if (c + 1 >= ntc) break;
+      step(c + 1, st1, st0);
+      if (c + 2 >= ntc) break;
     }
   }
 
-  // Value drift s C_vk q in the output layout: C_vk in its buffer (folded; staged here only
-  // when there was no tile) or staged over the tables' LDS.
-  if constexpr (FOLD) {
-    if (!cvk_staged) stage_matrix(a.cvk + (int64_t)bank * D * D);
-  } else {
-    __syncthreads();
-    stage_matrix(a.cvk + (int64_t)bank * D * D);
-  }
+  // Value drift s C_vk q in the output layout: stage C_vk over the tables' LDS.
+  __syncthreads();
+  stage_matrix(a.cvk + (int64_t)bank * D * D);
   staged_barrier();
 
   const float l = pair_sum(lsum);

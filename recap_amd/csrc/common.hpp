@@ -163,14 +163,14 @@ typedef __attribute__((address_space(3))) void lds_void;
 // Word 3 of a raw buffer resource on CDNA (32-bit data format, no swizzle).
 constexpr int kBufferRsrcWord3 = 0x00020000;
 
-// Coarse-tail table tiles: 32 key blocks (slots) per tile.  K-bar and w tiles are K-tile
-// rows (TileGeom<D>::k_off with the slot as the row); the V-bar tile is transposed,
-// [D][32 positions] with 64-byte rows, position p holding slot swap23(p), and 16-byte chunks
-// XOR-swizzled by bits 2-3 of the row.
+// Coarse-tail tables: one row per key block, and 32 blocks (slots) per tile of the coarse
+// kernel, which gathers the rows of a tile into K-tile images (TileGeom<D>::k_off with the
+// slot as the row).
 constexpr int kCoarseSlots = 32;
-__host__ __device__ inline int coarse_vt_off(int d, int pos) {  // bytes
-  return d * 64 + (((pos >> 3) ^ ((d >> 2) & 3)) << 4) + ((pos & 7) << 1);
-}
+
+// Four 16-bit elements in LDS, the operand of the transposing LDS read.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 s16x4_lds;
 
 __device__ inline u32x4 lds_load16(const char* base, int off) {
   return *reinterpret_cast<const u32x4*>(base + off);

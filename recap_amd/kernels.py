@@ -286,8 +286,8 @@ COARSE_SLOTS = 32  # key blocks per coarse-tail table tile
 
 
 def coarse_tables(var: torch.Tensor, kv: PackedKV, rank: int):
-    """w, kbar, vbar as tile images [banks, ceil(nb/32)*32, width] (see recap_coarse_tables;
-    w is [.., 16] in the folded form)."""
+    """w, kbar, vbar tables [banks, ceil(nb/32)*32, width], one row per key block (see
+    recap_coarse_tables; w is [.., 16] in the folded form)."""
     var = var.to(torch.float32).contiguous()
     banks, nb, d = var.shape
     padded = -(-nb // COARSE_SLOTS) * COARSE_SLOTS

@@ -277,6 +277,11 @@ def test_coarse_tail(cuda, name, rank):
     qt = K.basis_tables(basis.to(cuda), cvk.to(cuda), kv.dtype, query=True, cvk_table=True)
     wt, kbar, vbar = K.coarse_tables(var.to(cuda), kv, rank)
     assert wt.shape[-1] == (16 if 1 <= rank <= 13 and kv.dtype == torch.bfloat16 else wl.dim)
+    nb = kv.k_means.shape[1]  # one table row per key block, zero rows after the last
+    for table, means in ((kbar, kv.k_means), (vbar, kv.v_means)):
+        assert torch.equal(table[:, :nb], means.to(kv.dtype)), f"table rows {name}"
+        assert not table[:, nb:].any()
+    assert not wt[:, nb:].any()
     tables = {"w": wt, "kbar": kbar, "vbar": vbar, "u_t": qt.u_t, "cvk_t": qt.cvk_t,
               "rank": rank}
     glref = torch.randn(kl.shape[0], rows, generator=torch.Generator().manual_seed(3)).to(cuda)
