@@ -13,13 +13,14 @@
 // (recap/sparse/planner.py:24-27 is the host sync this removes).
 //
 // One workgroup = one (bank, 128-row query block), 4 waves x 32 rows.  The contractions
-// per 32-block tile (q.kbar, qsq.w, p.vbar, and one MFMA that puts -inf on the padding
-// slots' scores) run on 32x32x16 MFMA with the same register-resident layout trick as the
-// attention kernel: the fp32 result of one MFMA is the B operand of the next, the w table's
+// per 32-block tile (q.kbar, qsq.w, p.vbar) run on 32x32x16 MFMA with the same
+// register-resident layout trick as the attention kernel: the fp32 result of one MFMA is the B operand of the next, the w table's
 // columns are stored in the matching swap23 order, and vbar is read slot-major through the
 // transposing LDS read.  The tile loop is pipelined: a tile's score chains run on the
 // matrix cores while the previous tile's softmax runs on the VALU.  Also writes per-block
 // partial sums of (gl - gl_ref) for the per-bank drift centre (recap/operator.py:148-150).
+#include <array>
+
 #include "kernels.hpp"
 
 namespace recap {
@@ -158,11 +159,11 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
   // the tables (rows of the query type, one per key block): each lane copies the 16-byte
   // chunk its LDS position holds, K-tile layout with the compacted slot as the row, so kbar,
   // vbar and w images read exactly like packed tiles.  Padding slots read table row 0 and
-  // are masked.  The loop is pipelined across tiles: while the softmax and p.vbar of tile
-  // i run, the q.kbar and qsq.w chains of tile i+1 run on the matrix cores, so a wave's
-  // MFMAs overlap its own VALU work.  Tile i lives in stage i % 2 (layout: kbar, vbar, w
-  // images); its kbar and w images arrive two tiles ahead (they are read one tile ahead), its
-  // vbar image one tile ahead.
+  // are masked on the last tile.  The loop is pipelined across tiles: while the softmax and
+  // p.vbar of tile i run, the q.kbar and qsq.w chains of tile i+1 run on the matrix cores,
+  // so a wave's MFMAs overlap its own VALU work.  Tile i lives in stage i % 2 (layout: kbar,
+  // vbar, w images); its kbar and w images arrive two tiles ahead (they are read one tile
+  // ahead), its vbar image one tile ahead.
   const int ntc = (n_om + kCoarseSlots - 1) / kCoarseSlots;
   const int bank_tab = ntiles * kTabBytes;
   const int64_t tab_elems = (int64_t)bank * ntiles * kCoarseSlots * D;
@@ -209,18 +210,6 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
-  // Operands of the bias MFMA that starts each tile's q.kbar accumulator: A[slot][0] = -inf
-  // for a padding slot, 0 for a block; B[0][row] = 1; every other element of A and B is 0,
-  // so no -inf meets a 0.  The product is -inf on the padding slots and +0 on the others,
-  // where the chain then runs exactly as from a zero accumulator; a padding slot stays -inf
-  // through the chain and gets p = exp2(-inf) = 0 with no per-score select.
-  const unsigned bias_kept = g == 0 ? pack2<T>(-INFINITY, 0.0f) : 0u;
-  const u32x4 bias_ones = u32x4{g == 0 ? pack2<T>(1.0f, 0.0f) : 0u, 0u, 0u, 0u};
-  // Slots of tile c that hold a block (bit s), 0 past the last tile.
-  auto omit_word = [&](int c) -> unsigned {
-    const int left = n_om - kCoarseSlots * c;
-    return left >= kCoarseSlots ? ~0u : (left > 0 ? (1u << left) - 1u : 0u);
-  };
 
   // qsq = (U^T q)^2 in the query type (rotated value rounded, then its square rounded):
   // lane (g, l32) holds dims 32 ot + mfma_row(rr, g) of its row.  Full form: qsq in the
@@ -244,15 +233,20 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
       acc = T::mfma32(matrix_frag(ot, 2 * s + g), qreg[s], acc);
     float sq[16];
 #pragma unroll
-    for (int rr = 0; rr < 16; ++rr) {
-      const float x = T::to_f(T::from_f(acc[rr]));
-      sq[rr] = T::to_f(T::from_f(x * x));
+    for (int rr = 0; rr < 16; rr += 2) {
+      float x0 = acc[rr], x1 = acc[rr + 1];
+      round2<T>(x0, x1);
+      sq[rr] = x0 * x0;
+      sq[rr + 1] = x1 * x1;
+      if constexpr (FOLD) round2<T>(sq[rr], sq[rr + 1]);  // the full form rounds in pack2
     }
     if constexpr (FOLD) {
+      // The folded form has rank <= 13 (< 16 <= mfma_row(rr >= 8, g)): only the first
+      // eight registers of the first row tile can hold a leading dimension.
 #pragma unroll
       for (int rr = 0; rr < 16; ++rr) {
         const int c = 32 * ot + mfma_row(rr, g);
-        if (c < a.rank) frow[c] = sq[rr];
+        if (ot == 0 && rr < 8 && c < a.rank) frow[c] = sq[rr];
         else tail += sq[rr];
       }
     } else {
@@ -297,36 +291,34 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
   const float c1 = s32 * kLog2e, c2 = half * kLog2e;
   const float ln_full = logf((float)kBlock);
   const float short2 = (logf((float)(a.n_video - kBlock * (a.nb - 1))) - ln_full) * kLog2e;
-  // Block nb - 1, when omitted, is the last of the list: slot sl of tile short_tile, held by
-  // register short_reg of the lanes of half g = (sl / 4) % 2 (sl = mfma_row(short_reg, g)),
-  // which add its log2(n / 128) in units of c1.
-  const bool short_omitted = n_om > 0 && olist[n_om - 1] == a.nb - 1;
-  const int short_tile = short_omitted && short2 != 0.0f ? (n_om - 1) / kCoarseSlots : -1;
-  const int short_slot = (n_om - 1) % kCoarseSlots;
-  const int short_reg = 4 * (short_slot >> 3) + (short_slot & 3);
-  const float short_lane = g == ((short_slot >> 2) & 1) ? short2 / c1 : 0.0f;
+  // Only the last tile holds padding slots (n_last of its 32 slots hold blocks) and, when
+  // block nb - 1 is omitted, that short block, last in the list, at slot n_last - 1: it gets
+  // its log2(n / 128) added to its q.kbar score (units of c1).
+  const int n_last = n_om - kCoarseSlots * (ntc - 1);
+  const bool short_omitted = n_om > 0 && olist[n_om - 1] == a.nb - 1 && short2 != 0.0f;
+  const int fix_tile = n_last < kCoarseSlots || short_omitted ? ntc - 1 : -1;
+  const int short_slot = short_omitted ? n_last - 1 : -1;
+  const float short_add = short2 / c1;
 
-  // The score chains of the tile in stage `st`: s = q.kbar from the bias, quad = qsq.w.
-  // MFMA i of the chain: 0 the bias; folded, 1 the quad and 2 .. NS+1 the q.kbar slices;
-  // full, q.kbar slice s at 2s+1 and qsq.w slice s at 2s+2 (each chain in slice order).
-  constexpr int kScoreMfmas = FOLD ? NS + 2 : 2 * NS + 1;
-  auto score_frag = [&](const char* st, int i) {  // A operand of MFMA i >= 1
+  // The score chains of the tile in stage `st`: s = q.kbar, quad = qsq.w, each from a zero
+  // accumulator.  MFMA i of the chains: folded, 0 the quad and 1 .. NS the q.kbar slices;
+  // full, q.kbar slice s at 2s and qsq.w slice s at 2s+1 (each chain in slice order).
+  constexpr int kScoreMfmas = FOLD ? NS + 1 : 2 * NS;
+  auto score_frag = [&](const char* st, int i) {  // A operand of MFMA i
     if constexpr (FOLD) {
-      return i == 1 ? lds_load16(st + 2 * kTabBytes, 32 * l32 + 16 * g)
-                    : lds_load16(st, G::k_off(l32, 2 * (i - 2) + g));
+      return i == 0 ? lds_load16(st + 2 * kTabBytes, 32 * l32 + 16 * g)
+                    : lds_load16(st, G::k_off(l32, 2 * (i - 1) + g));
     } else {
-      return lds_load16(st + ((i - 1) & 1 ? 2 * kTabBytes : 0), G::k_off(l32, 2 * ((i - 1) >> 1) + g));
+      return lds_load16(st + (i & 1 ? 2 * kTabBytes : 0), G::k_off(l32, 2 * (i >> 1) + g));
     }
   };
-  auto score_mfma = [&](int i, const u32x4& f, const u32x4& bias_a, f32x16& sacc, f32x16& wacc) {
-    if (i == 0) {
-      sacc = T::mfma32(bias_a, bias_ones, f32x16{});
-    } else if constexpr (FOLD) {
-      if (i == 1) wacc = T::mfma32(f, qsq_pk[0], wacc);
-      else sacc = T::mfma32(f, qreg[i - 2], sacc);
+  auto score_mfma = [&](int i, const u32x4& f, f32x16& sacc, f32x16& wacc) {
+    if constexpr (FOLD) {
+      if (i == 0) wacc = T::mfma32(f, qsq_pk[0], f32x16{});
+      else sacc = T::mfma32(f, qreg[i - 1], i == 1 ? f32x16{} : sacc);
     } else {
-      if ((i - 1) & 1) wacc = T::mfma32(f, qsq_pk[(i - 1) >> 1], wacc);
-      else sacc = T::mfma32(f, qreg[(i - 1) >> 1], sacc);
+      if (i & 1) wacc = T::mfma32(f, qsq_pk[i >> 1], i == 1 ? f32x16{} : wacc);
+      else sacc = T::mfma32(f, qreg[i >> 1], i == 0 ? f32x16{} : sacc);
     }
   };
   // A operand of the p.vbar MFMA (output tile dt, slot half hh): rows 32 dt + l32 (value
@@ -378,17 +370,19 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) oacc[dt] = f32x16{};
 
-  // Lane (g, l32) holds slots mfma_row(rr, g); padding slots hold s = -inf.  The log-count
-  // ln 128 common to every full block is left out of the scores and added to the LSE at the
-  // end (softmax, gated share and output do not depend on it); the short last block gets
-  // its log2(n / 128) added to its q.kbar score (units of c1).
-  auto short_fix = [&](int c, f32x16& sacc) {
-    if (c == short_tile) {
-      int sreg = short_reg;
-      asm volatile("" : "+s"(sreg));  // keeps the 16 compares in this rare branch
+  // Lane (g, l32) holds slots mfma_row(rr, g).  The log-count ln 128 common to every full
+  // block is left out of the scores and added to the LSE at the end (softmax, gated share
+  // and output do not depend on it).  On the last tile, a rare branch gives the padding
+  // slots s = -inf (p = exp2(-inf) = 0) and the short block its log-count.
+  auto tail_fix = [&](int c, f32x16& sacc) {
+    if (c == fix_tile) {
+      int nl = n_last, ss = short_slot;
+      asm volatile("" : "+s"(nl), "+s"(ss));  // keeps the compares in this rare branch
 #pragma unroll
-      for (int rr = 0; rr < 16; ++rr)
-        if (rr == sreg) sacc[rr] += short_lane;
+      for (int rr = 0; rr < 16; ++rr) {
+        const int slot = mfma_row(rr, g);
+        sacc[rr] = slot >= nl ? -INFINITY : (slot == ss ? sacc[rr] + short_add : sacc[rr]);
+      }
     }
   };
   // Probability of slot register rr against m2: score - m2 = c1 s + (gate ? c2 quad : 0) - m2,
@@ -402,26 +396,27 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
     gpart += gate ? p[rr] : 0.0f;
   };
 
-  // The score chains of the tile in stage `st` (slot word ow) into sn/wn.  With a softmax
-  // to do (`probs`), the first pass of the probabilities of the current tile's scores
-  // (sacc/wacc) is spread over the chain: each MFMA is followed by one or two slots'
-  // probabilities, so the wave issues them while the MFMA runs (the chain's MFMAs depend
-  // on each other), and the A operands are read from LDS two MFMAs ahead.
-  auto scores = [&](const char* st, unsigned ow, f32x16& sn, f32x16& wn, auto probs,
-                    const f32x16& sacc, const f32x16& wacc, float* p, float& part,
+  // The score chains of the tile in stage `st` into sn/wn, from its first two A operands
+  // (f01, read from LDS by the caller).  With a softmax to do (`probs`), the first pass of
+  // the probabilities of the current tile's scores (sacc/wacc) is spread over the chain:
+  // each MFMA is followed by one or two slots' probabilities, so the wave issues them while
+  // the MFMA runs (the chain's MFMAs depend on each other), and the A operands are read
+  // from LDS two MFMAs ahead.
+  auto first_frags = [&](const char* st) {
+    return std::array<u32x4, 2>{score_frag(st, 0), score_frag(st, 1)};
+  };
+  auto scores = [&](const char* st, const std::array<u32x4, 2>& f01, f32x16& sn, f32x16& wn,
+                    auto probs, const f32x16& sacc, const f32x16& wacc, float* p, float& part,
                     float& gpart) {
-    // Lane (g, l32) holds A[slot l32][8g .. 8g+7] of the bias MFMA.
-    const u32x4 bias_a = u32x4{(ow >> l32) & 1u ? 0u : bias_kept, 0u, 0u, 0u};
     u32x4 f[3];
-    f[1] = score_frag(st, 1);
-    f[2] = score_frag(st, 2);
-    wn = f32x16{};
+    f[0] = f01[0];
+    f[1] = f01[1];
     part = 0.0f;
     gpart = 0.0f;
 #pragma unroll
     for (int i = 0; i < kScoreMfmas; ++i) {
-      if (i >= 1 && i + 2 < kScoreMfmas) f[(i + 2) % 3] = score_frag(st, i + 2);
-      score_mfma(i, f[i % 3], bias_a, sn, wn);
+      if (i + 2 < kScoreMfmas) f[(i + 2) % 3] = score_frag(st, i + 2);
+      score_mfma(i, f[i % 3], sn, wn);
       if constexpr (decltype(probs)::value) {
 #pragma unroll
         for (int rr = 16 * i / kScoreMfmas; rr < 16 * (i + 1) / kScoreMfmas; ++rr)
@@ -482,12 +477,13 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
   f32x16 sacc, wacc;
   auto step = [&](int c, char* cur, char* nxt) {
     tile_barrier();
+    const std::array<u32x4, 2> f01 = first_frags(nxt);
     if (c + 2 < ntc) copy_kw(c + 2, cur);
     if (c + 1 < ntc) copy_v(c + 1, nxt);
-    short_fix(c, sacc);
+    tail_fix(c, sacc);
     f32x16 sn, wn;
     float p[16], part, gpart;
-    scores(nxt, omit_word(c + 1), sn, wn, std::true_type{}, sacc, wacc, p, part, gpart);
+    scores(nxt, f01, sn, wn, std::true_type{}, sacc, wacc, p, part, gpart);
     finish_tile(cur, sacc, wacc, p, part, gpart);
     sacc = sn;
     wacc = wn;
@@ -499,7 +495,7 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
     tile_barrier();
     {
       float p[16], part, gpart;
-      scores(st0, omit_word(0), sacc, wacc, std::false_type{}, sacc, wacc, p, part, gpart);
+      scores(st0, first_frags(st0), sacc, wacc, std::false_type{}, sacc, wacc, p, part, gpart);
     }
     for (int c = 0;; c += 2) {
       step(c, st0, st1);
@@ -530,13 +526,25 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
       dacc = T::mfma32(matrix_frag(dt, 2 * s + g), qreg[s], dacc);
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
-      float v[4];
+      // o = (oacc / l) and gd = g * (drift) with drift = (dacc) * s, each (.) rounded to
+      // the query type; two values per conversion.
+      float o[4], dv[4], v[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float o = has_tail ? T::to_f(T::from_f(oacc[dt][4 * q4 + e] * inv_l)) : 0.0f;
-        const float dv = T::to_f(T::from_f(T::to_f(T::from_f(dacc[4 * q4 + e])) * a.scale));
-        const float gd = T::to_f(T::from_f(gfrac * dv));
-        v[e] = o + gd;
+        o[e] = oacc[dt][4 * q4 + e] * inv_l;
+        dv[e] = dacc[4 * q4 + e];
+      }
+#pragma unroll
+      for (int e = 0; e < 4; e += 2) {
+        round2<T>(o[e], o[e + 1]);
+        round2<T>(dv[e], dv[e + 1]);
+        dv[e] *= a.scale;
+        dv[e + 1] *= a.scale;
+        round2<T>(dv[e], dv[e + 1]);
+        float gd0 = gfrac * dv[e], gd1 = gfrac * dv[e + 1];
+        round2<T>(gd0, gd1);
+        v[e] = (has_tail ? o[e] : 0.0f) + gd0;
+        v[e + 1] = (has_tail ? o[e + 1] : 0.0f) + gd1;
       }
       *reinterpret_cast<u32x2*>(gorow + 32 * dt + 8 * q4 + 4 * g) =
           u32x2{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3])};

@@ -67,6 +67,20 @@ __device__ inline unsigned pack2(float lo, float hi) {
   }
 }
 
+// Two fp32 values each rounded to the 16-bit type (to nearest even) and widened back: one
+// conversion per pair.
+template <class T>
+__device__ inline void round2(float& lo, float& hi) {
+  const unsigned u = pack2<T>(lo, hi);
+  if constexpr (T::code == 2) {
+    lo = __uint_as_float(u << 16);
+    hi = __uint_as_float(u & 0xffff0000u);
+  } else {
+    lo = T::to_f((uint16_t)u);
+    hi = T::to_f((uint16_t)(u >> 16));
+  }
+}
+
 // ---------------------------------------------------------------------------------------
 // 32x32 MFMA output layout (all v_mfma_f32_32x32x* ops): lane l, register r holds
 // D[row = 8*(r/4) + 4*(l/32) + r%4][col = l%32].  A operand: lane l holds 8 consecutive
