@@ -103,52 +103,58 @@ __global__ __launch_bounds__(256, 2) void coarse_kernel(CoarseArgs a) {
   // olist: block j's place is the number of omitted blocks before it, i.e. the counts of the
   // earlier (chunk of 256, wave) pairs, scanned by one wave, plus the omitted lanes below it
   // in its ballot.  All of the row's loads are issued before the first ballot, and the Q
-  // row (which waits only for the row-map entry) in between.
+  // row (which waits only for the row-map entry) in between.  Rows of up to 1,024 blocks
+  // (every shape here) take a copy of the scan unrolled over 4 chunks instead of 16.
   u32x4 qreg[NS];
   int n_om;
   {
     const uint8_t* prow = a.partition + ((int64_t)bank * a.nb + qt) * a.nb;
     const int nchunks = (a.nb + 255) / 256;
-    uint8_t cell[kScan];
+    auto compact = [&](auto nc_tag) {
+      constexpr int NC = decltype(nc_tag)::value;  // chunks unrolled (>= nchunks)
+      uint8_t cell[NC];
 #pragma unroll
-    for (int i = 0; i < kScan; ++i) cell[i] = prow[min(256 * i + t, a.nb - 1)];  // in the row
-    const uint16_t* qrow = a.q + b * a.sB + h * a.sH + (int64_t)nat * a.sN;
+      for (int i = 0; i < NC; ++i) cell[i] = prow[min(256 * i + t, a.nb - 1)];  // in the row
+      const uint16_t* qrow = a.q + b * a.sB + h * a.sH + (int64_t)nat * a.sN;
 #pragma unroll
-    for (int s = 0; s < NS; ++s) qreg[s] = *reinterpret_cast<const u32x4*>(qrow + 16 * s + 8 * g);
-    unsigned flags = 0;
+      for (int s = 0; s < NS; ++s) qreg[s] = *reinterpret_cast<const u32x4*>(qrow + 16 * s + 8 * g);
+      unsigned flags = 0;
 #pragma unroll
-    for (int i = 0; i < kScan; ++i)
-      if (256 * i + t < a.nb && cell[i] == 0) flags |= 1u << i;
+      for (int i = 0; i < NC; ++i)
+        if (256 * i + t < a.nb && cell[i] == 0) flags |= 1u << i;
 #pragma unroll
-    for (int i = 0; i < kScan; ++i) {
-      if (i < nchunks) {  // uniform
-        const unsigned long long bal = __ballot((flags >> i) & 1u);
-        if (lane == 0) counts[4 * i + wave] = (int)__popcll(bal);
+      for (int i = 0; i < NC; ++i) {
+        if (i < nchunks) {  // uniform
+          const unsigned long long bal = __ballot((flags >> i) & 1u);
+          if (lane == 0) counts[4 * i + wave] = (int)__popcll(bal);
+        }
       }
-    }
-    __syncthreads();
-    if (wave == 0) {  // exclusive prefix of the 4 * nchunks counts, the total after them
-      const int n = 4 * nchunks;
-      const int own = lane < n ? counts[lane] : 0;
-      int v = own;
+      __syncthreads();
+      if (wave == 0) {  // exclusive prefix of the 4 * nchunks counts, the total after them
+        const int n = 4 * nchunks;
+        const int own = lane < n ? counts[lane] : 0;
+        int v = own;
 #pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const int u = __shfl_up(v, off, 64);
-        if (lane >= off) v += u;
+        for (int off = 1; off < 4 * NC; off <<= 1) {
+          const int u = __shfl_up(v, off, 64);
+          if (lane >= off) v += u;
+        }
+        if (lane < n) counts[lane] = v - own;
+        if (lane == 4 * NC - 1) counts[4 * kScan] = v;
       }
-      if (lane < n) counts[lane] = v - own;
-      if (lane == 63) counts[4 * kScan] = v;
-    }
-    __syncthreads();
+      __syncthreads();
 #pragma unroll
-    for (int i = 0; i < kScan; ++i) {
-      if (i < nchunks) {  // uniform
-        const unsigned long long bal = __ballot((flags >> i) & 1u);
-        if ((flags >> i) & 1u)
-          olist[counts[4 * i + wave] + (int)__popcll(bal & ((1ull << lane) - 1ull))] =
-              (uint16_t)(256 * i + t);
+      for (int i = 0; i < NC; ++i) {
+        if (i < nchunks) {  // uniform
+          const unsigned long long bal = __ballot((flags >> i) & 1u);
+          if ((flags >> i) & 1u)
+            olist[counts[4 * i + wave] + (int)__popcll(bal & ((1ull << lane) - 1ull))] =
+                (uint16_t)(256 * i + t);
+        }
       }
-    }
+    };
+    if (nchunks <= 4) compact(std::integral_constant<int, 4>{});
+    else compact(std::integral_constant<int, kScan>{});
     n_om = __builtin_amdgcn_readfirstlane(counts[4 * kScan]);
     if (t < kCoarseSlots) olist[n_om + t] = 0;  // padding slots read table row 0
   }

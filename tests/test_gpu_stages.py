@@ -16,7 +16,7 @@ from gpu_util import (SMALL, assert_parity, banks_view, k_tile_to_rows, metrics,
 from recap_amd import _lib
 from recap_amd import kernels as K
 from recap_amd.layout import Layout, hilbert_permutation
-from recap_amd.synthetic import WORKLOADS, make_qkv
+from recap_amd.synthetic import WORKLOADS, Workload, make_qkv
 
 pytestmark = pytest.mark.gpu
 
@@ -25,8 +25,14 @@ STAGE1_CASES = [("tiny", None), ("text-first-ragged", None), ("text-last-d128", 
                 ("hunyuan-720p", [0, 1])]
 
 
+# A video-only shape whose rows hold 1,101 blocks: the coarse kernel scans partition rows of
+# more than 1,024 blocks with its 16-chunk code.
+LONG = {"long-row-d64": Workload("long-row-d64", 1, 64, (4, 35, 1006), 0, False, 0.25,
+                                 torch.bfloat16)}
+
+
 def _setup(name, heads, cuda, seed=0, dtype=None):
-    wl = SMALL.get(name) or WORKLOADS[name]
+    wl = SMALL.get(name) or LONG.get(name) or WORKLOADS[name]
     dtype = dtype or (torch.bfloat16 if wl.dtype == torch.float32 else wl.dtype)
     print(f"case {name} heads={heads} N={wl.tokens} d={wl.dim}", flush=True)
     q, k, v = make_qkv(wl, heads=heads, seed=seed, dtype=dtype)
@@ -251,7 +257,7 @@ def test_closure_statistics(cuda, name):
 @pytest.mark.parametrize("name,rank", [("tiny", 4), ("text-first-ragged", 4),
                                        ("text-last-d128", 4), ("video-ragged-d128", 4),
                                        ("text-last-d128", 0), ("text-last-d128", 13),
-                                       ("video-ragged-d128", 20)])
+                                       ("video-ragged-d128", 20), ("long-row-d64", 4)])
 def test_coarse_tail(cuda, name, rank):
     """The coarse kernel against the oracle fed with the same closure statistics.  Ranks
     1-13 take the folded w table (16 features) in bf16, the others the full one."""
@@ -289,8 +295,33 @@ def test_coarse_tail(cuda, name, rank):
     assert_parity(go.cpu().float(), go_ref[:, :rows], f"coarse {name}")
     fin = torch.isfinite(gl_ref[:, :rows])
     assert torch.equal(torch.isfinite(gl.cpu()), fin)
-    m, _ = metrics(gl.cpu()[fin], gl_ref[:, :rows][fin])
-    assert m < 2e-3, m
+    err = torch.where(fin, (gl.cpu() - gl_ref[:, :rows]).abs(), torch.zeros(()))
+    bad = err > 2e-3
+    if bad.any():
+        # The gate fl(s^2 qsq.w) <= theta^2 is discontinuous: the other decision moves a
+        # block's logit by up to theta^2 / 2.  Two causes can flip it, and a row that differs
+        # must match the oracle under one of them, for its query blocks:
+        # (a) two fp32 summation orders of qsq.w (~1e-7 relative) on a pair at the threshold:
+        #     theta^2 moved by 1e-5 one way or the other;
+        # (b) qsq itself: the reference's U^T q is a bf16 GEMM whose fp32 accumulation order
+        #     is open (recap/sparse/closure.py:84-86), and one element of it can round to the
+        #     neighbouring bf16 value; qsq from an MFMA-accumulated GEMM on the GPU.
+        blocks = sorted({int(r) // 128 for r in torch.nonzero(bad.any(0)).flatten()})
+        ub = O.cast(basis, torch.bfloat16).to(torch.bfloat16).to(cuda)
+        rot = torch.stack([qv[i].to(torch.bfloat16).to(cuda) @ ub[i].contiguous()
+                           for i in range(qv.shape[0])]).float().cpu()
+        qsq_gemm = O.cast(rot * rot, torch.bfloat16)
+        rel = 1e-5
+        alternates = [(qsq, 2.0 * math.sqrt(1.0 + rel)), (qsq, 2.0 * math.sqrt(1.0 - rel)),
+                      (qsq_gemm, 2.0)]
+        best = torch.full_like(err, math.inf)
+        for qsq_alt, th in alternates:
+            _, gl_alt = O.coarse_tail(ql, qsq_alt, drift, km_ref, vm_ref, w, counts, part, scale,
+                                      th, wl.video_tokens, torch.bfloat16, query_blocks=blocks)
+            best = torch.minimum(best, (gl.cpu() - gl_alt[:, :rows]).abs())
+        print(f"  gl: {int(bad.sum())} rows over 2e-3 (max {float(err.max()):.3e}); against "
+              f"the gate and qsq alternates max {float(best[bad].max()):.3e}", flush=True)
+        assert float(best[bad].max()) < 2e-3, float(best[bad].max())
     center = K.drift_center(dpart, geo)
     cref = O.drift_center(gl.cpu(), glref.cpu())
     assert torch.allclose(center.cpu(), cref, atol=1e-4, rtol=1e-4)
