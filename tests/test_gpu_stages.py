@@ -28,6 +28,9 @@ STAGE1_CASES = [("tiny", None), ("text-first-ragged", None), ("text-last-d128", 
 # A video-only shape whose rows hold 1,101 blocks: the coarse kernel scans partition rows of
 # more than 1,024 blocks with its 16-chunk code.
 LONG = {"long-row-d64": Workload("long-row-d64", 1, 64, (4, 35, 1006), 0, False, 0.25,
+                                 torch.bfloat16),
+        # 71 video blocks, the last one ragged (40 tokens)
+        "mid-row-d128": Workload("mid-row-d128", 2, 128, (3, 25, 120), 0, False, 0.2,
                                  torch.bfloat16)}
 
 
@@ -325,3 +328,58 @@ def test_coarse_tail(cuda, name, rank):
     center = K.drift_center(dpart, geo)
     cref = O.drift_center(gl.cpu(), glref.cpu())
     assert torch.allclose(center.cpu(), cref, atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("name", ["tiny", "text-last-d128", "mid-row-d128"])
+def test_coarse_tail_extreme_partitions(cuda, name):
+    """The coarse kernel on partitions the selection never makes but the kernel must take:
+    query blocks that keep every block (no tail: output 0, LSE -inf), that keep only
+    themselves (every other block omitted, the last one ragged), that omit 1 to 40 blocks
+    (a partial tile, a full one, one more), against the oracle on the same partition."""
+    wl, (q, k, v), (qg, kg, vg), rowmap, fwd, geo = _setup(name, None, cuda)
+    scale, rank = scale_for(wl.dim), 4
+    kv = K.kv_pack(kg, vg, rowmap, geo)
+    ql, kl, vl = (banks_view(x, fwd) for x in (q, k, v))
+    km_ref, counts = O.pool_blocks(kl, wl.video_tokens)
+    vm_ref, _ = O.pool_blocks(vl, wl.video_tokens)
+    basis = O.closure_basis(O.within_block_scatter(kl, km_ref, counts, wl.video_tokens))
+    _, var = O.rotated_moments(kl, basis, counts, wl.video_tokens)
+    basis, var = O.order_basis(basis, var, counts)
+    cvk = O.value_key_covariance(kl, vl, km_ref, counts, wl.video_tokens)
+    w = O.fold_rank(var, rank)
+    nb = km_ref.shape[1]
+    part = O.head_partition(ql, kl, scale, wl.density, wl.video_tokens).clone()
+    g = torch.Generator().manual_seed(11)
+    for i in range(nb):
+        kind = i % 4
+        if kind == 0:
+            part[:, i] = True                               # nothing omitted
+        elif kind == 1:
+            part[:, i] = False
+            part[:, i, i] = True                            # all but the block itself
+        elif kind == 2:
+            part[:, i] = True
+            n_om = min((1, 2, 31, 32, 33, 40)[(i // 4) % 6], nb - 1)
+            omit = torch.randperm(nb, generator=g)[:n_om]
+            part[:, i, omit] = False                        # 1 .. 40 omitted
+    qv = ql[:, :wl.video_tokens].float()
+    qsq = O.rotated_query_square(qv, basis, torch.bfloat16)
+    drift = O.value_drift(qv, cvk, scale, torch.bfloat16)
+    go_ref, gl_ref = O.coarse_tail(ql, qsq, drift, km_ref, vm_ref, w, counts, part, scale, 2.0,
+                                   wl.video_tokens, torch.bfloat16)
+    rows = geo.rows
+    qt = K.basis_tables(basis.to(cuda), cvk.to(cuda), kv.dtype, query=True, cvk_table=True)
+    wt, kbar, vbar = K.coarse_tables(var.to(cuda), kv, rank)
+    tables = {"w": wt, "kbar": kbar, "vbar": vbar, "u_t": qt.u_t, "cvk_t": qt.cvk_t,
+              "rank": rank}
+    glref = torch.zeros(kl.shape[0], rows, device=cuda)
+    go, gl, _ = K.coarse_tail(qg, rowmap, part.to(cuda), geo, tables, scale, 2.0, glref)
+    assert_parity(go.cpu().float(), go_ref[:, :rows], f"coarse extreme {name}")
+    fin = torch.isfinite(gl_ref[:, :rows])
+    assert torch.equal(torch.isfinite(gl.cpu()), fin)
+    empty = ~(~part).any(-1)                                # [banks, nb] query blocks, no tail
+    erows = empty.repeat_interleave(128, dim=1)[:, :rows]
+    assert erows.any() and not fin[erows].any()
+    assert not go.cpu()[erows].any()
+    m, _ = metrics(gl.cpu()[fin], gl_ref[:, :rows][fin])
+    assert m < 2e-3, m
