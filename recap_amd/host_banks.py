@@ -168,22 +168,31 @@ class HostBankOperator(Operator):
                     if tensor is not None and tensor.data_ptr() != views[name].data_ptr():
                         views[name].copy_(tensor.reshape(views[name].shape))
                 self._pager("stage_out", bank_key, slot, compute)
+                if not load:
+                    # A refresh that loaded nothing prefetched nothing; with its bank on its
+                    # way out, the next stored bank (after the stream's last layer, layer 0
+                    # of the next step) can come in while the step ends.
+                    self._prefetch_after(layer_index, stored_only=True)
         finally:
             self._pager("release", slot, compute)
             for name in FIELDS:
                 setattr(bank, name, None)
         return out
 
-    def _prefetch_after(self, layer: int) -> None:
+    def _prefetch_after(self, layer: int, stored_only: bool = False) -> None:
         """Bring the next layer's bank into the other slot while this layer computes; after
-        the stream's last layer the next is layer 0 of the following step."""
+        the stream's last layer the next is layer 0 of the following step.  With
+        `stored_only`, only a bank that host memory already holds."""
         if len(self._slots) < 2:
             return
         n_layers = len(self.layers[self.stream])
         nxt = layer + 1 if layer + 1 < n_layers else 0
         if nxt % len(self._slots) == layer % len(self._slots):
             return
-        self._pager("prefetch", self._key(self.stream, nxt), nxt % len(self._slots))
+        key = self._key(self.stream, nxt)
+        if stored_only and not self._pager.stored(key):
+            return
+        self._pager("prefetch", key, nxt % len(self._slots))
 
     # -- bookkeeping ---------------------------------------------------------------------
 
