@@ -41,6 +41,13 @@ constexpr int kMaxTiles = 2048;
 // stays below 2^8, exact in fp32 and bf16, and the O rescale is skipped.
 constexpr float kRescaleSlack = 8.0f;
 
+// At d = 64 a step has half the MFMA work of d = 128 for the same softmax work per score,
+// so the VALU bounds it.  There the running max is instead raised only when a sub-tile's
+// probabilities, taken against the current max, sum to more than kSumCap in some lane (or
+// are not finite): the sub-tile is then redone against its own max, and no row max is taken
+// on the common path (every accepted p is <= kSumCap, exact in fp32 and bf16).
+constexpr float kSumCap = 4096.0f;
+
 // s_waitcnt immediate (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
 // that waits for all vector memory operations of this wave -- the tile copies into LDS --
 // and all its LDS reads.
@@ -407,6 +414,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
                   auto next_tag, auto parity_tag) __attribute__((always_inline)) {
     constexpr bool kNext = decltype(next_tag)::value;
     constexpr bool kOdd = decltype(parity_tag)::value;
+    constexpr bool kSumCheck = D == 64;
     if (it + 1 < nsub) copy(vrs, image(it + 1), kOdd ? v_lds0 : v_lds1);
     if (it + 2 < nsub) copy(krs, image(it + 2), kOdd ? k_lds1 : k_lds0);
     const char* kl = kOdd ? k_lds0 : k_lds1;   // K_{it+1}
@@ -445,6 +453,43 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
           part[q][kt] = (pp & 7) ? part[q][kt] + (p0 + p1) : p0 + p1;
           w[q][kt][hh][e >> 1] = pack2<T>(p0, p1);
         }
+        if constexpr (kSumCheck) {
+          // After the slice with the last pair, before any PV MFMA reads them: a lane whose
+          // probabilities overflow the cap (or are not finite, as when m = -inf) redoes the
+          // sub-tile against the raised running max, rescaling O and l first.
+          if ((n + 1) * PPS >= NPAIR) {
+            bool over = false;
+#pragma unroll
+            for (int q = 0; q < kGroups; ++q) over |= !(part[q][0] + part[q][1] <= kSumCap);
+            if (__any(over)) {
+              __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+              for (int q = 0; q < kGroups; ++q) {
+                float mx = -INFINITY;
+#pragma unroll
+                for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                  for (int rr = 0; rr < 16; ++rr) mx = __builtin_elementwise_maximum(mx, cur[q][kt][rr]);
+                const float mnew = pair_max(mx) * a.scale_log2;
+                if (mnew > m[q]) {
+                  const float alpha = __builtin_amdgcn_exp2f(m[q] - mnew);
+                  lsum[q] *= alpha;
+#pragma unroll
+                  for (int dt = 0; dt < NDT; ++dt) oacc[q][dt] *= alpha;
+                  m[q] = mnew;
+                }
+#pragma unroll
+                for (int pp = 0; pp < 16; ++pp) {
+                  const int kt = pp >> 3, hh = (pp >> 2) & 1, e = 2 * (pp & 3);
+                  const float p0 = __builtin_amdgcn_exp2f(fmaf(cur[q][kt][8 * hh + e], a.scale_log2, -m[q]));
+                  const float p1 = __builtin_amdgcn_exp2f(fmaf(cur[q][kt][8 * hh + e + 1], a.scale_log2, -m[q]));
+                  part[q][kt] = (pp & 7) ? part[q][kt] + (p0 + p1) : p0 + p1;
+                  w[q][kt][hh][e >> 1] = pack2<T>(p0, p1);
+                }
+              }
+            }
+          }
+        }
       }
       if (n < NQK) {
         const int st = n >> 1, kt = n & 1;
@@ -464,7 +509,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
           const u32x4 pk = {w[q][kt][hh][0], w[q][kt][hh][1], w[q][kt][hh][2], w[q][kt][hh][3]};
           oacc[q][dt] = T::mfma32(fr[n % 3], pk, oacc[q][dt]);
         }
-        if constexpr (kNext) {
+        if constexpr (kNext && !kSumCheck) {
           // Row max over MPS pairs of S_{it+1} scores (pair mp: group mp % kGroups).
 #pragma unroll
           for (int mp = i * MPS; mp < (i + 1) * MPS; ++mp) {
@@ -480,7 +525,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnArgs a) {
     if constexpr (MODE == kModeDenseHead) {
       if (it + 1 == kept_end) store_head();
     }
-    if constexpr (kNext) {
+    if constexpr (kNext && !kSumCheck) {
 #pragma unroll
       for (int q = 0; q < kGroups; ++q) update_max(q, mx[q]);
     }
