@@ -16,6 +16,7 @@ line.
 from __future__ import annotations
 
 import argparse
+import gc
 import hashlib
 import json
 import math
@@ -369,12 +370,17 @@ def main() -> int:
     log("[bench] warmup done")
     op.stage_events = {}
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # No garbage collection inside the timed calls: a collection pauses the host for ~10-20
+    # ms, which drains the launch queue of a short call (1.7 ms at the Wan shape).
+    gc.collect()
+    gc.disable()
     torch.cuda.synchronize()
     start.record()
     for _ in range(args.steps):
         op.attend(0, q1, k1, v1)
     end.record()
     torch.cuda.synchronize()
+    gc.enable()
     ms = start.elapsed_time(end) / args.steps
     stages = elapsed_stages(op.stage_events)
     ev = op.stage_events
