@@ -34,14 +34,25 @@ LONG = {"long-row-d64": Workload("long-row-d64", 1, 64, (4, 35, 1006), 0, False,
                                  torch.bfloat16)}
 
 
-def _setup(name, heads, cuda, seed=0, dtype=None):
+def _setup(name, heads, cuda, seed=0, dtype=None, k_factors=None):
+    """Inputs of workload ``name``; with ``k_factors``, the keys of reordered block i are
+    scaled by ``k_factors[i % len(k_factors)]`` (in fp32, before the cast)."""
     wl = SMALL.get(name) or LONG.get(name) or WORKLOADS[name]
     dtype = dtype or (torch.bfloat16 if wl.dtype == torch.float32 else wl.dtype)
-    print(f"case {name} heads={heads} N={wl.tokens} d={wl.dim}", flush=True)
-    q, k, v = make_qkv(wl, heads=heads, seed=seed, dtype=dtype)
+    print(f"case {name} heads={heads} N={wl.tokens} d={wl.dim} k_factors={k_factors}",
+          flush=True)
     perm = hilbert_permutation(wl.grid)
     layout = Layout.from_permutation(perm, text_tokens=wl.text_tokens, text_first=wl.text_first)
     fwd, _ = O.gather_indices(perm, wl.text_tokens, wl.text_first)
+    if k_factors is None:
+        q, k, v = make_qkv(wl, heads=heads, seed=seed, dtype=dtype)
+    else:
+        q, k, v = make_qkv(wl, heads=heads, seed=seed, dtype=torch.float32)
+        f = torch.tensor(k_factors)[(torch.arange(wl.tokens) // 128) % len(k_factors)]
+        native = torch.empty(wl.tokens)
+        native[fwd] = f
+        k = k * native.view(1, 1, -1, 1)
+        q, k, v = (x.to(dtype) for x in (q, k, v))
     geo = K.Geometry(wl.tokens, wl.video_tokens)
     return wl, (q, k, v), tuple(x.to(cuda) for x in (q, k, v)), layout.rowmap(cuda), fwd, geo
 
@@ -216,6 +227,46 @@ def test_attention_modes_short_and_ragged(cuda, n, d, keep_last):
         assert m < 2e-3, m
 
 
+@pytest.mark.parametrize("d", [64, 128])
+def test_attention_running_max_jumps(cuda, d):
+    """Keys of each 64-key sub-tile scaled by factors from 0.1 to 80, so that a row's scores
+    rise by tens of log2 units between sub-tiles (and fall): the lazy running max (d = 128),
+    the probability-sum check with its redo (d = 64), and the dense-head pass's head snapshot
+    in the middle of such a walk, in head, dense and dense-head modes against the oracle."""
+    n, banks = 1000, 2
+    print(f"case n={n} d={d}", flush=True)
+    g = torch.Generator().manual_seed(17 + d)
+    tb = -(-n // 128)
+    q, k, v = (torch.randn(1, banks, n, d, generator=g) for _ in range(3))
+    factors = torch.tensor([1.0, 8.0, 0.25, 24.0, 2.0, 40.0, 0.5, 12.0, 3.0, 60.0, 1.0, 0.1,
+                            16.0, 5.0, 80.0, 1.0])
+    k = k * factors[torch.arange(n) // 64].view(1, 1, n, 1)
+    q, k, v = (x.to(torch.bfloat16) for x in (q, k, v))
+    kmask = torch.rand(banks, tb, tb, generator=g) > 0.4
+    kmask[:, torch.arange(tb), torch.arange(tb)] = True
+    geo = K.Geometry(n, n)
+    rowmap = torch.arange(n, dtype=torch.int32, device=cuda)
+    kv = K.kv_pack(k.to(cuda), v.to(cuda), rowmap, geo)
+    scale = scale_for(d)
+    ql, kl, vl = (x[0].float() for x in (q, k, v))
+    ref, ref_lse = O.block_sparse_attention(ql, kl, vl, kmask, scale)
+    dref, dref_lse = O.dense_attention(ql, kl, vl, scale)
+    head, head_lse = K.block_sparse_attn(q.to(cuda), kv, rowmap, kmask.to(cuda), geo, scale)
+    assert_parity(head.cpu().float(), ref, "head")
+    dense, dlse = K.dense_attn(q.to(cuda), kv, rowmap, scale)
+    assert_parity(dense.cpu().float()[0], dref, "dense")
+    fd, flse, fh, fhlse = K.dense_head_attn(q.to(cuda), kv, rowmap, kmask.to(cuda), scale)
+    assert torch.equal(fh, head) and torch.equal(fhlse, head_lse)
+    assert_parity(fd.cpu().float()[0], dref, "dense-head: dense")
+    for got, want in ((head_lse, ref_lse), (dlse[0], dref_lse), (flse[0], dref_lse)):
+        # the scores reach a few hundred: fp32 accumulation of their products
+        err = (got.cpu().double() - want.double()).abs()
+        bound = 2e-3 + 1e-5 * want.double().abs()
+        print(f"  lse max-abs {float(err.max()):.3e} (|lse| up to "
+              f"{float(want.abs().max()):.1f})", flush=True)
+        assert bool((err <= bound).all()), float((err - bound).max())
+
+
 def test_dense_attention_matches_torch_sdpa(cuda):
     wl = SMALL["text-last-d128"]
     q, k, v = (x.to(cuda) for x in make_qkv(wl, seed=1))
@@ -264,7 +315,20 @@ def test_closure_statistics(cuda, name):
 def test_coarse_tail(cuda, name, rank):
     """The coarse kernel against the oracle fed with the same closure statistics.  Ranks
     1-13 take the folded w table (16 features) in bf16, the others the full one."""
-    wl, (q, k, v), (qg, kg, vg), rowmap, fwd, geo = _setup(name, None, cuda)
+    _check_coarse_tail(cuda, name, rank)
+
+
+@pytest.mark.parametrize("name", ["mid-row-d128", "long-row-d64"])
+def test_coarse_tail_score_jumps(cuda, name):
+    """Keys of each block scaled by factors from 0.5 to 10, so that the coarse scores jump by
+    tens of log2 units between tiles of omitted blocks, up and down: the probability-sum
+    check and its redo under a raised running max, against the oracle."""
+    _check_coarse_tail(cuda, name, 4, k_factors=(1.0, 3.0, 0.5, 6.0, 1.5, 10.0, 0.75, 4.0))
+
+
+def _check_coarse_tail(cuda, name, rank, k_factors=None):
+    wl, (q, k, v), (qg, kg, vg), rowmap, fwd, geo = _setup(name, None, cuda,
+                                                          k_factors=k_factors)
     scale = scale_for(wl.dim)
     kv = K.kv_pack(kg, vg, rowmap, geo)
     ql, kl, vl = (banks_view(x, fwd) for x in (q, k, v))
