@@ -31,11 +31,15 @@ __global__ __launch_bounds__(closure_threads(D, FLAGS), 1) void closure_kernel(C
   constexpr int NTHR = closure_threads(D, FLAGS);
   constexpr bool SPLIT = NTHR == 512;
   constexpr bool KC = SCAT;  // centred keys staged in LDS (the scatter's A and B operands)
-  __shared__ __attribute__((aligned(16))) char k_lds[G::kTileBytes];
-  __shared__ __attribute__((aligned(16))) char v_lds[CVK ? G::kTileBytes : 16];
+  constexpr int NSLOT = SCAT ? 2 : 4;  // 64-key halves of the K / V^T tiles in LDS
+  constexpr int KH = G::kHalfBytes, VH = CVK ? G::kHalfBytes : 16;
+  __shared__ __attribute__((aligned(16))) char k_s0[KH], k_s1[KH];
+  __shared__ __attribute__((aligned(16))) char k_s2[NSLOT > 2 ? KH : 16], k_s3[NSLOT > 2 ? KH : 16];
+  __shared__ __attribute__((aligned(16))) char v_s0[VH], v_s1[VH];
+  __shared__ __attribute__((aligned(16))) char v_s2[NSLOT > 2 ? VH : 16], v_s3[NSLOT > 2 ? VH : 16];
   __shared__ __attribute__((aligned(16))) char kc_hi[KC ? D * 256 : 16];
   __shared__ __attribute__((aligned(16))) char kc_lo[KC ? D * 256 : 16];
-  __shared__ float kmean_s[D];
+  __shared__ float kmean_s[2][D];
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, g = lane >> 5, l32 = lane & 31;
   const int bank = blockIdx.x / a.groups, grp = blockIdx.x % a.groups;
@@ -98,55 +102,122 @@ __global__ __launch_bounds__(closure_threads(D, FLAGS), 1) void closure_kernel(C
 #pragma unroll
   for (int i = 0; i < (SCAT ? NT : 1); ++i) sacc[i] = f32x16{};
 
-  // The next block's K (and V^T) tile and mean are loaded into registers while this block
-  // is processed, then stored into LDS at the top of the next iteration.
-  constexpr int KCH = G::kTileBytes / 16 / NTHR;  // 16-byte chunks per thread per tile
-  u32x4 kpre[KCH], vpre[CVK ? KCH : 1];
-  float mpre = 0.0f;
-  auto load_block = [&](int j) {
-    const u32x4* ks = reinterpret_cast<const u32x4*>(a.kp + ((int64_t)bank * a.tb + j) * G::kTileElems);
-#pragma unroll
-    for (int i = 0; i < KCH; ++i) kpre[i] = ks[t + NTHR * i];
-    if constexpr (CVK) {
-      const u32x4* vs = reinterpret_cast<const u32x4*>(a.vp + ((int64_t)bank * a.tb + j) * G::kTileElems);
-#pragma unroll
-      for (int i = 0; i < KCH; ++i) vpre[i] = vs[t + NTHR * i];
-    }
-    if (t < D) mpre = a.kmean[((int64_t)bank * a.nb + j) * D + t];
+  // The K and V^T tiles stream through NSLOT slots of one 64-key half each (a half of
+  // either image is contiguous), copied straight into LDS by buffer loads, so NSLOT - 1
+  // halves are in flight while one is processed.  Each slot is an array of its own, so the
+  // compiler can tell that a half's LDS reads miss the copies in flight.  The statistics
+  // are taken per half in the order of the whole-block computation (tiles tt = 2 hf and
+  // 2 hf + 1 of half hf, the rotated moments reduced after the second half), so the results
+  // do not depend on the split.  A block's key mean is copied the same way, one block ahead,
+  // into one of two LDS rows (block parity).
+  constexpr int HCH = G::kHalfBytes / 16 / NTHR;  // 16-byte copies per thread per image half
+  constexpr int NDMA = HCH * (CVK ? 2 : 1);        // copies per thread per half
+  constexpr bool MEAN = CVK || SCAT;
+  const int nh = 2 * max(j1 - j0, 0);
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.kp + (int64_t)bank * a.tb * G::kTileElems), 0, a.tb * G::kTileBytes,
+      kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.vp + (int64_t)bank * a.tb * G::kTileElems), 0, CVK ? a.tb * G::kTileBytes : 0,
+      kBufferRsrcWord3);
+  auto slot_k = [&](auto u) -> char* {
+    constexpr int U = decltype(u)::value % NSLOT;
+    if constexpr (U == 0) return k_s0;
+    else if constexpr (U == 1) return k_s1;
+    else if constexpr (U == 2) return k_s2;
+    else return k_s3;
   };
-  if (j0 < j1) load_block(j0);
-  for (int j = j0; j < j1; ++j) {
-    __syncthreads();
+  auto slot_v = [&](auto u) -> char* {
+    constexpr int U = decltype(u)::value % NSLOT;
+    if constexpr (U == 0) return v_s0;
+    else if constexpr (U == 1) return v_s1;
+    else if constexpr (U == 2) return v_s2;
+    else return v_s3;
+  };
+  auto copy_half = [&](int h, char* kdst, char* vdst) {
+    const int src = (j0 + (h >> 1)) * G::kTileBytes + (h & 1) * G::kHalfBytes;
 #pragma unroll
-    for (int i = 0; i < KCH; ++i) reinterpret_cast<u32x4*>(k_lds)[t + NTHR * i] = kpre[i];
-    if constexpr (CVK) {
-#pragma unroll
-      for (int i = 0; i < KCH; ++i) reinterpret_cast<u32x4*>(v_lds)[t + NTHR * i] = vpre[i];
+    for (int i = 0; i < HCH; ++i) {
+      const int lo = 16 * (NTHR * i + 64 * wave), off = src + 16 * (NTHR * i + t);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void*)(kdst + lo), 16, off, 0, 0, 0);
+      if constexpr (CVK)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void*)(vdst + lo), 16, off, 0, 0, 0);
     }
-    if (t < D) kmean_s[t] = mpre;
-    if (j + 1 < j1) load_block(j + 1);
+  };
+  // This wave's copies but its last N have landed and its LDS writes are done; then every
+  // wave has passed the same point.  Copies land in order, and any other vector memory
+  // access counted after them only makes the wait longer.
+  auto vm_barrier = [&](auto n_tag) {
+    constexpr int N = decltype(n_tag)::value;
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4));  // vmcnt(N) lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  auto lds_barrier = [&]() {  // LDS writes of every wave done, copies left in flight
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (0x7 << 4));  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  const __amdgpu_buffer_rsrc_t mrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.kmean + (int64_t)bank * a.nb * D), 0, MEAN ? a.nb * D * 4 : 0, kBufferRsrcWord3);
+  auto copy_mean = [&](int j) {  // wave 0, 16 bytes per lane
+    if (t < D / 4)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(mrs, (lds_void*)kmean_s[(j - j0) & 1], 16,
+                                               4 * j * D + 16 * t, 0, 0, 0);
+  };
+  if (nh > 0) {
+    if constexpr (MEAN) copy_mean(j0);
+    copy_half(0, k_s0, v_s0);
+    copy_half(1, k_s1, v_s1);
+    if constexpr (NSLOT == 4)
+      if (nh > 2) copy_half(2, k_s2, v_s2);
+  }
+
+  // Half h of the group, in slot U % NSLOT (hf = U % 2 is h % 2: NSLOT is even and every
+  // pass of the loop starts at a multiple of NSLOT): the copies and barriers every wave takes
+  // part in, then this wave's `work`.
+  auto half = [&](auto u, int h, auto& work) {
+    constexpr int U = decltype(u)::value, HF = U & 1;
+    const char* ks = slot_k(u);
+    const char* vs = slot_v(u);
+    const int jb = h >> 1, j = j0 + jb;
+    // Copies issued after those of half h: halves h + 1 .. min(h + NSLOT - 2, nh - 1), and
+    // the next block's mean, issued before them, has landed by the same count.
+    const int ahead = min(NSLOT - 2, nh - 1 - h);
+    if (NSLOT == 4 && ahead >= 2) vm_barrier(std::integral_constant<int, 2 * NDMA>{});
+    else if (NSLOT == 4 && ahead == 1) vm_barrier(std::integral_constant<int, NDMA>{});
+    else vm_barrier(std::integral_constant<int, 0>{});
+    if constexpr (MEAN)
+      if (HF == 0 && j + 1 < j1) copy_mean(j + 1);
+    // The slot of half h + NSLOT - 1 held half h - 1, which every wave has finished.
+    if (h + NSLOT - 1 < nh)
+      copy_half(h + NSLOT - 1, slot_k(std::integral_constant<int, U + NSLOT - 1>{}),
+                slot_v(std::integral_constant<int, U + NSLOT - 1>{}));
     const int count = min(kBlock, a.n_video - j * kBlock);
-    __syncthreads();
+    const float* kmean_b = kmean_s[jb & 1];
 
     if constexpr (KC) {
-      // Centred keys, transposed to [D][128 positions] (position p holds key swap23(p)).
-      for (int cc = t; cc < D * 16; cc += NTHR) {
-        const int n = cc >> 4, c = cc & 15;
+      // Centred keys, transposed to [D][128 positions] (position p holds key swap23(p), in
+      // the same half as p): positions 64 hf .. 64 hf + 63 here.
+      for (int cc = t; cc < D * 8; cc += NTHR) {
+        const int n = cc >> 3, c = 8 * HF + (cc & 7);
         unsigned whi[4], wlo[4];
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
           float hv[2], lv[2];
 #pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            const int key = swap23(8 * c + e + u);
+          for (int w = 0; w < 2; ++w) {
+            const int key = swap23(8 * c + e + w);
             float x = 0.0f;
             if (key < count) {
               const uint16_t raw = *reinterpret_cast<const uint16_t*>(
-                  k_lds + G::k_off(key, n >> 3) + ((n & 7) << 1));
-              x = T::to_f(raw) - kmean_s[n];
+                  ks + G::k_off(key - 64 * HF, n >> 3) + ((n & 7) << 1));
+              x = T::to_f(raw) - kmean_b[n];
             }
-            hv[u] = T::to_f(T::from_f(x));
-            lv[u] = x - hv[u];
+            hv[w] = T::to_f(T::from_f(x));
+            lv[w] = x - hv[w];
           }
           whi[e >> 1] = pack2<T>(hv[0], hv[1]);
           wlo[e >> 1] = pack2<T>(lv[0], lv[1]);
@@ -154,63 +225,77 @@ __global__ __launch_bounds__(closure_threads(D, FLAGS), 1) void closure_kernel(C
         *reinterpret_cast<u32x4*>(kc_hi + G::vt_off(n, c)) = u32x4{whi[0], whi[1], whi[2], whi[3]};
         *reinterpret_cast<u32x4*>(kc_lo + G::vt_off(n, c)) = u32x4{wlo[0], wlo[1], wlo[2], wlo[3]};
       }
-      __syncthreads();
+      lds_barrier();
     }
+    work(u, ks, vs, j, count, kmean_b);
+  };
 
+  // A wave has one job (rot_tile or mat_tile) for the whole group, and each job runs its own
+  // copy of the loop, so the registers one job keeps from half to half (the rotated tiles of
+  // the block, or the C_vk accumulators) are not held through the other job's code.
+  f32x16 racc[ROT ? 4 : 1];
+  auto rot_work = [&](auto u, const char* ks, const char*, int j, int count, const float*) {
+    constexpr int HF = decltype(u)::value & 1;
     if constexpr (ROT) {
-      if (rot_tile >= 0) {
-        f32x16 racc[4];
+      {
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
+        for (int w = 0; w < 2; ++w) {
+          const int tt = 2 * HF + w;
           racc[tt] = f32x16{};
 #pragma unroll
           for (int s = 0; s < NS; ++s) {
-            const u32x4 ka = lds_load16(k_lds, G::k_off(32 * tt + l32, 2 * s + g));
+            const u32x4 ka = lds_load16(ks, G::k_off(32 * w + l32, 2 * s + g));
             racc[tt] = T::mfma32(ka, ub[s], racc[tt]);
           }
 #pragma unroll
           for (int s = 0; s < NS; ++s) {
-            const u32x4 ka = lds_load16(k_lds, G::k_off(32 * tt + l32, 2 * s + g));
+            const u32x4 ka = lds_load16(ks, G::k_off(32 * w + l32, 2 * s + g));
             racc[tt] = T::mfma32(ka, ub[NS + s], racc[tt]);
           }
         }
-        float s1 = 0.0f;
+        if constexpr (HF == 1) {
+          float s1 = 0.0f;
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
+          for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-          for (int rr = 0; rr < 16; ++rr)
-            if (32 * tt + mfma_row(rr, g) < count) s1 += racc[tt][rr];
-        const float fc = (float)count;
-        const float mean = pair_sum(s1) / fc;
-        float s2 = 0.0f;
+            for (int rr = 0; rr < 16; ++rr)
+              if (32 * tt + mfma_row(rr, g) < count) s1 += racc[tt][rr];
+          const float fc = (float)count;
+          const float mean = pair_sum(s1) / fc;
+          float s2 = 0.0f;
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
+          for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-          for (int rr = 0; rr < 16; ++rr)
-            if (32 * tt + mfma_row(rr, g) < count) {
-              const float dlt = racc[tt][rr] - mean;
-              s2 += dlt * dlt;
-            }
-        const float var = fmaxf(pair_sum(s2) / fc, 0.0f);
-        if (g == 0) a.var[((int64_t)bank * a.nb + j) * D + 32 * rot_tile + l32] = var;
+            for (int rr = 0; rr < 16; ++rr)
+              if (32 * tt + mfma_row(rr, g) < count) {
+                const float dlt = racc[tt][rr] - mean;
+                s2 += dlt * dlt;
+              }
+          const float var = fmaxf(pair_sum(s2) / fc, 0.0f);
+          if (g == 0) a.var[((int64_t)bank * a.nb + j) * D + 32 * rot_tile + l32] = var;
+        }
       }
     }
-
+  };
+  auto mat_work = [&](auto u, const char* ks, const char* vs, int, int count,
+                      const float* kmean_b) {
+    constexpr int HF = decltype(u)::value & 1;
     if constexpr (CVK) {
-      if (mat_tile >= 0) {
+      {
         // C_vk[:, n] for this wave's 32 columns n.  The centred keys come from the matrix
         // core: the K rows times an identity slice, accumulated onto -kbar[n], land in the
         // output layout (lane = column n, registers = 16 tokens in swap23 order), which is
         // the B operand of V^T Kc against the V^T tile's positions -- no transpose in LDS.
-        const float neg_mean = -kmean_s[32 * mat_tile + l32];
+        const float neg_mean = -kmean_b[32 * mat_tile + l32];
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
+        for (int w = 0; w < 2; ++w) {
+          const int tt = 2 * HF + w;
           f32x16 kc;
 #pragma unroll
           for (int r = 0; r < 16; ++r) kc[r] = neg_mean;
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh)
-            kc = T::mfma32(lds_load16(k_lds, G::k_off(32 * tt + l32, 4 * mat_tile + 2 * hh + g)),
+            kc = T::mfma32(lds_load16(ks, G::k_off(32 * w + l32, 4 * mat_tile + 2 * hh + g)),
                            bid[hh], kc);
           if (count < kBlock) {
 #pragma unroll
@@ -232,11 +317,12 @@ __global__ __launch_bounds__(closure_threads(D, FLAGS), 1) void closure_kernel(C
             bhi[hh] = u32x4{whi[0], whi[1], whi[2], whi[3]};
             blo[hh] = u32x4{wlo[0], wlo[1], wlo[2], wlo[3]};
           }
+          // V^T positions 32 tt + 16 hh .. of this half: chunk 4 w + 2 hh + g of its image.
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
             for (int mt = 0; mt < NT; ++mt) {
-              const u32x4 va = lds_load16(v_lds, G::vt_off(32 * mt + l32, 4 * tt + 2 * hh + g));
+              const u32x4 va = lds_load16(vs, G::vt_off(32 * mt + l32, 4 * w + 2 * hh + g));
               f32x16 c = cget(mt);
               c = T::mfma32(va, bhi[hh], c);
               cset(mt, T::mfma32(va, blo[hh], c));
@@ -245,10 +331,10 @@ __global__ __launch_bounds__(closure_threads(D, FLAGS), 1) void closure_kernel(C
       }
     }
     if constexpr (SCAT) {
-      if (mat_tile >= 0) {
+      {
         const int nrow = 32 * mat_tile + l32;
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
+        for (int s = 4 * HF; s < 4 * HF + 4; ++s) {
           const u32x4 ahi = lds_load16(kc_hi, G::vt_off(nrow, 2 * s + g));
           const u32x4 alo = lds_load16(kc_lo, G::vt_off(nrow, 2 * s + g));
 #pragma unroll
@@ -262,7 +348,22 @@ __global__ __launch_bounds__(closure_threads(D, FLAGS), 1) void closure_kernel(C
         }
       }
     }
-  }
+  };
+  auto idle = [&](auto, const char*, const char*, int, int, const float*) {};
+  auto run = [&](auto work) {
+    for (int h0 = 0; h0 < nh; h0 += NSLOT) {
+      half(std::integral_constant<int, 0>{}, h0, work);
+      half(std::integral_constant<int, 1>{}, h0 + 1, work);
+      if constexpr (NSLOT == 4) {
+        if (h0 + 2 >= nh) break;
+        half(std::integral_constant<int, 2>{}, h0 + 2, work);
+        half(std::integral_constant<int, 3>{}, h0 + 3, work);
+      }
+    }
+  };
+  if (ROT && rot_tile >= 0) run(rot_work);
+  else if ((CVK || SCAT) && mat_tile >= 0) run(mat_work);
+  else run(idle);
 
   if (mat_tile >= 0) {
     const int64_t pbase = ((int64_t)bank * a.groups + grp) * D * D;
