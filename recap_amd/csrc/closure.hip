@@ -195,7 +195,9 @@ __global__ __launch_bounds__(closure_threads(D, FLAGS), 1) void closure_kernel(C
     if (h + NSLOT - 1 < nh)
       copy_half(h + NSLOT - 1, slot_k(std::integral_constant<int, U + NSLOT - 1>{}),
                 slot_v(std::integral_constant<int, U + NSLOT - 1>{}));
-    const int count = min(kBlock, a.n_video - j * kBlock);
+    // Valid tokens of the block (kBlock except for a ragged last block), made scalar so that
+    // the masks below are branches taken by that block only.
+    const int count = __builtin_amdgcn_readfirstlane(min(kBlock, a.n_video - j * kBlock));
     const float* kmean_b = kmean_s[jb & 1];
 
     if constexpr (KC) {
@@ -254,24 +256,30 @@ __global__ __launch_bounds__(closure_threads(D, FLAGS), 1) void closure_kernel(C
           }
         }
         if constexpr (HF == 1) {
-          float s1 = 0.0f;
+          // Mean, then mean squared deviation, over the block's valid tokens in token-tile
+          // order; a full block (every block but a ragged last one) needs no mask.
+          auto moments = [&](auto full_tag) {
+            constexpr bool FULL = decltype(full_tag)::value;
+            float s1 = 0.0f;
 #pragma unroll
-          for (int tt = 0; tt < 4; ++tt)
+            for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-            for (int rr = 0; rr < 16; ++rr)
-              if (32 * tt + mfma_row(rr, g) < count) s1 += racc[tt][rr];
-          const float fc = (float)count;
-          const float mean = pair_sum(s1) / fc;
-          float s2 = 0.0f;
+              for (int rr = 0; rr < 16; ++rr)
+                if (FULL || 32 * tt + mfma_row(rr, g) < count) s1 += racc[tt][rr];
+            const float fc = (float)count;
+            const float mean = pair_sum(s1) / fc;
+            float s2 = 0.0f;
 #pragma unroll
-          for (int tt = 0; tt < 4; ++tt)
+            for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-            for (int rr = 0; rr < 16; ++rr)
-              if (32 * tt + mfma_row(rr, g) < count) {
-                const float dlt = racc[tt][rr] - mean;
-                s2 += dlt * dlt;
-              }
-          const float var = fmaxf(pair_sum(s2) / fc, 0.0f);
+              for (int rr = 0; rr < 16; ++rr)
+                if (FULL || 32 * tt + mfma_row(rr, g) < count) {
+                  const float dlt = racc[tt][rr] - mean;
+                  s2 = fmaf(dlt, dlt, s2);  // explicit: a contraction could fuse either product
+                }
+            return fmaxf(pair_sum(s2) / fc, 0.0f);
+          };
+          const float var = count == kBlock ? moments(std::true_type{}) : moments(std::false_type{});
           if (g == 0) a.var[((int64_t)bank * a.nb + j) * D + 32 * rot_tile + l32] = var;
         }
       }
@@ -302,7 +310,8 @@ __global__ __launch_bounds__(closure_threads(D, FLAGS), 1) void closure_kernel(C
             for (int r = 0; r < 16; ++r)
               if (32 * tt + mfma_row(r, g) >= count) kc[r] = 0.0f;
           }
-          // hi + lo pair of the centred key, as in the staged path.
+          // hi + lo pair of the centred key, as in the staged path: the hi pair is the packed
+          // rounding itself, widened back to form the lo pair.
           u32x4 bhi[2], blo[2];
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh) {
@@ -310,8 +319,9 @@ __global__ __launch_bounds__(closure_threads(D, FLAGS), 1) void closure_kernel(C
 #pragma unroll
             for (int e = 0; e < 8; e += 2) {
               const float x0 = kc[8 * hh + e], x1 = kc[8 * hh + e + 1];
-              const float h0 = T::to_f(T::from_f(x0)), h1 = T::to_f(T::from_f(x1));
-              whi[e >> 1] = pack2<T>(h0, h1);
+              float h0 = x0, h1 = x1;
+              round2<T>(h0, h1);
+              whi[e >> 1] = pack2<T>(x0, x1);
               wlo[e >> 1] = pack2<T>(x0 - h0, x1 - h1);
             }
             bhi[hh] = u32x4{whi[0], whi[1], whi[2], whi[3]};
