@@ -183,8 +183,10 @@ __global__ __launch_bounds__(closure_threads(D, FLAGS), 1) void closure_kernel(C
     const char* ks = slot_k(u);
     const char* vs = slot_v(u);
     const int jb = h >> 1, j = j0 + jb;
-    // Copies issued after those of half h: halves h + 1 .. min(h + NSLOT - 2, nh - 1), and
-    // the next block's mean, issued before them, has landed by the same count.
+    // Wait for half h: the copies issued after its own are those of halves h + 1 ..
+    // min(h + NSLOT - 2, nh - 1), plus at most one block mean, which only lengthens the wait.
+    // A block's mean is issued before the copy of its second half, so the wait for its first
+    // half, which leaves only copies of later halves outstanding, covers it.
     const int ahead = min(NSLOT - 2, nh - 1 - h);
     if (NSLOT == 4 && ahead >= 2) vm_barrier(std::integral_constant<int, 2 * NDMA>{});
     else if (NSLOT == 4 && ahead == 1) vm_barrier(std::integral_constant<int, NDMA>{});
