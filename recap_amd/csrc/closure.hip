@@ -39,7 +39,7 @@ __global__ __launch_bounds__(closure_threads(D, FLAGS), 1) void closure_kernel(C
   __shared__ __attribute__((aligned(16))) char v_s2[NSLOT > 2 ? VH : 16], v_s3[NSLOT > 2 ? VH : 16];
   __shared__ __attribute__((aligned(16))) char kc_hi[KC ? D * 256 : 16];
   __shared__ __attribute__((aligned(16))) char kc_lo[KC ? D * 256 : 16];
-  __shared__ float kmean_s[2][D];
+  __shared__ __attribute__((aligned(16))) float kmean_s[2][D];  // 16-byte copies land here
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, g = lane >> 5, l32 = lane & 31;
   const int bank = blockIdx.x / a.groups, grp = blockIdx.x % a.groups;
