@@ -242,20 +242,23 @@ __global__ __launch_bounds__(closure_threads(D, FLAGS), 1) void closure_kernel(C
     constexpr int HF = decltype(u)::value & 1;
     if constexpr (ROT) {
       {
+        // The half's K fragments are all requested before the first MFMA (the fence keeps
+        // the compiler from moving each read next to its use, where the MFMA would wait out
+        // the LDS latency); each serves the hi and the lo product.
+        u32x4 ka[2][NS];
+#pragma unroll
+        for (int w = 0; w < 2; ++w)
+#pragma unroll
+          for (int s = 0; s < NS; ++s) ka[w][s] = lds_load16(ks, G::k_off(32 * w + l32, 2 * s + g));
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int w = 0; w < 2; ++w) {
           const int tt = 2 * HF + w;
           racc[tt] = f32x16{};
 #pragma unroll
-          for (int s = 0; s < NS; ++s) {
-            const u32x4 ka = lds_load16(ks, G::k_off(32 * w + l32, 2 * s + g));
-            racc[tt] = T::mfma32(ka, ub[s], racc[tt]);
-          }
+          for (int s = 0; s < NS; ++s) racc[tt] = T::mfma32(ka[w][s], ub[s], racc[tt]);
 #pragma unroll
-          for (int s = 0; s < NS; ++s) {
-            const u32x4 ka = lds_load16(ks, G::k_off(32 * w + l32, 2 * s + g));
-            racc[tt] = T::mfma32(ka, ub[NS + s], racc[tt]);
-          }
+          for (int s = 0; s < NS; ++s) racc[tt] = T::mfma32(ka[w][s], ub[NS + s], racc[tt]);
         }
         if constexpr (HF == 1) {
           // Mean, then mean squared deviation, over the block's valid tokens in token-tile
@@ -300,13 +303,24 @@ __global__ __launch_bounds__(closure_threads(D, FLAGS), 1) void closure_kernel(C
 #pragma unroll
         for (int w = 0; w < 2; ++w) {
           const int tt = 2 * HF + w;
+          // The token tile's K and V^T fragments, all requested before its first MFMA (the
+          // fence keeps them there; V^T positions 32 tt + 16 hh .. of this half are chunk
+          // 4 w + 2 hh + g of its image).
+          u32x4 kf[2], va[2][NT];
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh)
+            kf[hh] = lds_load16(ks, G::k_off(32 * w + l32, 4 * mat_tile + 2 * hh + g));
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int mt = 0; mt < NT; ++mt)
+              va[hh][mt] = lds_load16(vs, G::vt_off(32 * mt + l32, 4 * w + 2 * hh + g));
+          __builtin_amdgcn_sched_barrier(0);
           f32x16 kc;
 #pragma unroll
           for (int r = 0; r < 16; ++r) kc[r] = neg_mean;
 #pragma unroll
-          for (int hh = 0; hh < 2; ++hh)
-            kc = T::mfma32(lds_load16(ks, G::k_off(32 * w + l32, 4 * mat_tile + 2 * hh + g)),
-                           bid[hh], kc);
+          for (int hh = 0; hh < 2; ++hh) kc = T::mfma32(kf[hh], bid[hh], kc);
           if (count < kBlock) {
 #pragma unroll
             for (int r = 0; r < 16; ++r)
@@ -329,15 +343,13 @@ __global__ __launch_bounds__(closure_threads(D, FLAGS), 1) void closure_kernel(C
             bhi[hh] = u32x4{whi[0], whi[1], whi[2], whi[3]};
             blo[hh] = u32x4{wlo[0], wlo[1], wlo[2], wlo[3]};
           }
-          // V^T positions 32 tt + 16 hh .. of this half: chunk 4 w + 2 hh + g of its image.
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
             for (int mt = 0; mt < NT; ++mt) {
-              const u32x4 va = lds_load16(vs, G::vt_off(32 * mt + l32, 4 * w + 2 * hh + g));
               f32x16 c = cget(mt);
-              c = T::mfma32(va, bhi[hh], c);
-              cset(mt, T::mfma32(va, blo[hh], c));
+              c = T::mfma32(va[hh][mt], bhi[hh], c);
+              cset(mt, T::mfma32(va[hh][mt], blo[hh], c));
             }
         }
       }
