@@ -63,8 +63,25 @@ def build(verbose: bool = True) -> Path:
         proc = subprocess.run(cmd, capture_output=True, text=True)
         if proc.returncode:
             raise RuntimeError("link failed:\n" + proc.stdout + proc.stderr)
+        missing = undefined_own_symbols(tmp_lib)
+        if missing:
+            raise RuntimeError("librecap_hip.so would leave symbols of its own undefined (a "
+                               "kernel's host launch stub was not emitted): " + ", ".join(missing))
         os.replace(tmp_lib, LIB)
     return LIB
+
+
+def undefined_own_symbols(lib: Path) -> list[str]:
+    """Symbols of the `recap` namespace that ``lib`` references but does not define.  The host
+    pass of a HIP source can drop a kernel's launch stub without an error; the library then
+    links and fails only when it is loaded."""
+    nm = shutil.which("nm") or "/opt/rocm/llvm/bin/llvm-nm"
+    proc = subprocess.run([nm, "-D", "--undefined-only", str(lib)], capture_output=True,
+                          text=True)
+    if proc.returncode:
+        raise RuntimeError(f"{nm} failed on {lib}: {proc.stderr}")
+    names = [line.split()[-1] for line in proc.stdout.splitlines() if line.strip()]
+    return [n for n in names if n.startswith("_ZN5recap")]
 
 
 if __name__ == "__main__":
