@@ -281,12 +281,18 @@ def test_dense_attention_matches_torch_sdpa(cuda):
 
 
 @pytest.mark.parametrize("name", ["tiny", "text-last-d128", "video-ragged-d128"])
-def test_closure_statistics(cuda, name):
+@pytest.mark.parametrize("group", [None, 3, 8])
+def test_closure_statistics(cuda, name, group):
+    """The three flag sets of the closure kernel against the oracle and each other, with
+    the default blocks per workgroup (one at these sizes) and with groups of 3 and 8 (a
+    partial last group, several blocks streamed through the kernel's four LDS slots)."""
     wl, (q, k, v), (qg, kg, vg), rowmap, fwd, geo = _setup(name, None, cuda)
+    print(f"  group {group}", flush=True)
     kv = K.kv_pack(kg, vg, rowmap, geo)
     kl, vl = banks_view(k, fwd), banks_view(v, fwd)
     km_ref, counts = O.pool_blocks(kl, wl.video_tokens)
-    _, cvk, scatter = K.closure_stats(kv, geo, _lib.CLOSURE_CVK | _lib.CLOSURE_SCATTER)
+    _, cvk, scatter = K.closure_stats(kv, geo, _lib.CLOSURE_CVK | _lib.CLOSURE_SCATTER,
+                                      group=group)
     scatter_ref = O.within_block_scatter(kl, km_ref, counts, wl.video_tokens)
     cvk_ref = O.value_key_covariance(kl, vl, km_ref, counts, wl.video_tokens)
     rel = float((scatter.cpu() - scatter_ref).abs().max() / scatter_ref.abs().max())
@@ -298,10 +304,15 @@ def test_closure_statistics(cuda, name):
     basis = O.closure_basis(scatter_ref)
     split = K.basis_tables(basis.to(cuda), None, kv.dtype, split=True)
     var, cvk2, _ = K.closure_stats(kv, geo, _lib.CLOSURE_ROT | _lib.CLOSURE_CVK, split.u_hi_t,
-                                   split.u_lo_t)
+                                   split.u_lo_t, group=group)
     assert torch.equal(cvk2, cvk)
-    var_only, _, _ = K.closure_stats(kv, geo, _lib.CLOSURE_ROT, split.u_hi_t, split.u_lo_t)
+    var_only, _, _ = K.closure_stats(kv, geo, _lib.CLOSURE_ROT, split.u_hi_t, split.u_lo_t,
+                                     group=group)
     assert torch.equal(var_only, var)
+    if group is not None:  # the variances do not depend on the grouping at all
+        var1, _, _ = K.closure_stats(kv, geo, _lib.CLOSURE_ROT, split.u_hi_t, split.u_lo_t,
+                                     group=1)
+        assert torch.equal(var1, var)
     _, var_ref = O.rotated_moments(kl, basis, counts, wl.video_tokens)
     rel = float(((var.cpu() - var_ref).abs() / (var_ref.abs() + 1e-3)).max())
     print(f"  rotated variance rel {rel:.2e}", flush=True)
