@@ -34,6 +34,15 @@ def test_library_exports_every_declared_symbol():
     assert lib.recap_abi_version() == _lib.ABI_VERSION
 
 
+def test_library_defines_its_own_symbols():
+    """Every symbol of the library's own namespace that it references is defined in it: a
+    HIP host pass can drop a kernel's launch stub without an error, which would otherwise
+    show only when a GPU process loads the library."""
+    from recap_amd.build_lib import LIB, undefined_own_symbols
+    assert LIB.exists(), "build librecap_hip.so first (python -m recap_amd.build_lib)"
+    assert undefined_own_symbols(LIB) == []
+
+
 def test_noalloc_capture_size_limit_is_checked_on_the_host():
     """recap_refresh_capture_noalloc rejects a validation whose partial pairs exceed its
     static scratch before it touches a device (the pointers here are never dereferenced)."""
