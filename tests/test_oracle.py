@@ -618,3 +618,94 @@ def test_rerank_branch_of_a_revalidating_refresh(min_overlap, expect_rerank):
     print(f"min_overlap={min_overlap}: sparse vs dense on the refresh inputs max {err.max():.2e}")
     assert float(op.last["center"].abs().max()) < 1e-6
     assert float(err.median()) < 1e-5 and float(err.max()) < 2e-2
+
+
+def _paired_block_keys(n: int, sigma: torch.Tensor, basis: torch.Tensor, g) -> torch.Tensor:
+    """n deviations (n even) from a block mean: +a_i and -a_i for n/2 vectors a_i chosen so
+    that the block's covariance (1/n) sum d d^T is exactly U diag(sigma^2) U^T and every odd
+    central moment vanishes."""
+    d = sigma.numel()
+    q, _ = torch.linalg.qr(torch.randn(n // 2, n // 2, generator=g, dtype=torch.float64))
+    a = math.sqrt(n / 2.0) * q[:, :d] * sigma.double().view(1, -1)   # a^T a = (n/2) diag(s^2)
+    y = torch.cat([a, -a])
+    return y @ basis.double().T
+
+
+def _expansion_case(eps: float, theta: float, drift_sign: float = 1.0):
+    """The coarse tail of one omitted block per query block against the exact attention
+    over that block's tokens, for keys k = kbar_b + U y (block covariance
+    eps^2 U diag(sigma^2) U^T, symmetric deviations) and values v = vbar_b + M (k - kbar_b).
+    Returns (max |lse - exact lse|, max |out - exact out|)."""
+    g = torch.Generator().manual_seed(77)
+    d, full = 16, 3
+    counts = torch.tensor([128.0] * full + [40.0])
+    nv = int(counts.sum())
+    basis, _ = torch.linalg.qr(torch.randn(d, d, generator=g, dtype=torch.float64))
+    # fold_rank(rank=4) keeps the 4 leading variances and averages the rest: equal trailing
+    # variances make the folded table exact, so q^T C q = qsq . w.
+    sigma = eps * torch.tensor([2.0, 1.6, 1.3, 1.1] + [0.7] * (d - 4), dtype=torch.float64)
+    means = torch.randn(counts.numel(), d, generator=g, dtype=torch.float64) * 0.6
+    mix = torch.randn(d, d, generator=g, dtype=torch.float64) * 0.5
+    k_rows, v_rows = [], []
+    vbar = torch.randn(counts.numel(), d, generator=g, dtype=torch.float64)
+    for b, n in enumerate(counts.int().tolist()):
+        dev = _paired_block_keys(n, sigma, basis, g)
+        k_rows.append(means[b] + dev)
+        v_rows.append(vbar[b] + dev @ mix.T)
+    k = torch.cat(k_rows).unsqueeze(0)
+    v = torch.cat(v_rows).unsqueeze(0)
+    q = torch.randn(1, nv, d, generator=g, dtype=torch.float64)
+    scale = 1.0 / math.sqrt(d)
+    kf, vf, qf = (x.float() for x in (k, v, q))
+    km, cnt = O.pool_blocks(kf, nv)
+    vm, _ = O.pool_blocks(vf, nv)
+    ub = basis.float().unsqueeze(0)
+    _, var = O.rotated_moments(kf, ub, cnt, nv)
+    cvk = O.value_key_covariance(kf, vf, km, cnt, nv)
+    qsq = O.rotated_query_square(qf, ub, torch.float32)
+    drift = O.value_drift(qf, cvk, scale, torch.float32) * drift_sign
+    nb = counts.numel()
+    part = torch.ones(1, nb, nb, dtype=torch.bool)
+    omitted = [(i + 1) % nb for i in range(nb)]
+    for i, j in enumerate(omitted):
+        part[0, i, j] = False
+    out, lse = O.coarse_tail(qf, qsq, drift, km, vm, O.fold_rank(var, 4), cnt, part, scale,
+                             theta, nv, torch.float32)
+    starts = torch.cumsum(torch.cat([torch.zeros(1), counts]), 0).long()
+    err_l = err_o = 0.0
+    for i, j in enumerate(omitted):
+        rows = slice(int(starts[i]), int(starts[i + 1]))
+        keys = slice(int(starts[j]), int(starts[j + 1]))
+        s = scale * (q[0, rows] @ k[0, keys].T)
+        exact_lse = torch.logsumexp(s, -1)
+        exact_out = torch.softmax(s, -1) @ v[0, keys]
+        err_l = max(err_l, float((lse[0, rows].double() - exact_lse).abs().max()))
+        err_o = max(err_o, float((out[0, rows].double() - exact_out).abs().max()))
+    return err_l, err_o
+
+
+def test_coarse_tail_corrections_follow_the_cumulant_expansion():
+    """The coarse tail's correction terms against the mathematics they approximate
+    (recap/kernels/coarse_tail.py:1-12, 128-141; recap/sparse/closure.py:1-9).  For one
+    omitted block b of n keys with mean kbar and within-block covariance C,
+    log sum_t exp(s q.k_t) = s q.kbar + ln n + (s^2/2) q^T C q + O(kappa_4 s^4): with
+    symmetric deviations the third cumulant vanishes, so the corrected log-mass misses by
+    O(eps^4) when the deviations scale by eps, the uncorrected one (gate closed) by O(eps^2).
+    With values v = vbar + M (k - kbar), the softmax-weighted value is vbar + s C_vk q +
+    O(eps^4): the drift term g s C_vk q leaves an O(eps^4) miss, without it (gate closed, so
+    g = 0) or with its sign flipped the miss is O(eps^2).  Halving eps must therefore divide
+    the corrected misses by about 16 and the others by about 4: a wrong coefficient, gate
+    direction, log-count or drift sign fails."""
+    eps = [0.4, 0.2, 0.1]
+    corrected = [_expansion_case(e, theta=2.0) for e in eps]
+    closed = [_expansion_case(e, theta=1e-6) for e in eps]
+    flipped = [_expansion_case(e, theta=2.0, drift_sign=-1.0) for e in eps]
+    for a, b in zip(corrected, corrected[1:]):
+        assert a[0] / b[0] > 11.0 and a[1] / b[1] > 11.0, corrected
+    for a, b in zip(closed, closed[1:]):
+        assert 3.0 < a[0] / b[0] < 5.5 and 3.0 < a[1] / b[1] < 5.5, closed
+    for a, b in zip(flipped, flipped[1:]):
+        assert 3.0 < a[1] / b[1] < 5.5, flipped
+    # the corrections remove nearly all of the miss at the smallest deviation
+    assert corrected[-1][0] < 0.02 * closed[-1][0] and corrected[-1][1] < 0.02 * closed[-1][1]
+    assert corrected[-1][1] < 0.02 * flipped[-1][1]
