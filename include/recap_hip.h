@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define RECAP_ABI_VERSION 7
+#define RECAP_ABI_VERSION 8
 
 enum { RECAP_OK = 0, RECAP_EINVAL = 1, RECAP_EUNSUPPORTED = 2, RECAP_EHIP = 3 };
 enum { RECAP_F16 = 1, RECAP_BF16 = 2 };
@@ -336,6 +336,13 @@ int recap_pager_counts(const recap_pager* pager, int64_t* counts);
 /* Total milliseconds of the timed copy batches and their number (RECAP_PAGER_TIMING);
  * waits for them.  No counterpart in the reference (its copies are untimed). */
 int recap_pager_copy_time(recap_pager* pager, double* total_ms, int64_t* copies);
+/* New field sizes for every key, after a change of the bank geometry (a per-prompt text
+ * length changes the kernel mask's [banks, tb, tb]).  Waits for the transfers in flight;
+ * every key then holds no bank (the next refresh writes one back), host fields that the
+ * new sizes outgrow are freed and reallocated on the next write-back, and every slot must
+ * be bound again.  Replaces the reallocation of the split state and of the host banks on a
+ * shape change, recap/host_banks.py:58-64, 116-146, 164-167. */
+int recap_pager_resize(recap_pager* pager, const int64_t* field_bytes, int32_t n_fields);
 
 /* Asynchronous copy of a refinement bank between pinned host memory and the device on
  * `stream` (hipMemcpyAsync, direction inferred).

@@ -11,7 +11,7 @@ import threading
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "librecap_hip.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 RECAP_OK, RECAP_EINVAL, RECAP_EUNSUPPORTED, RECAP_EHIP = 0, 1, 2, 3
 RECAP_F16, RECAP_BF16 = 1, 2
@@ -77,6 +77,7 @@ SIGNATURES: dict[str, tuple] = {
     "recap_pager_host_bytes": (_I64, [_P]),
     "recap_pager_counts": (_I, [_P, _P]),
     "recap_pager_copy_time": (_I, [_P, _P, _P]),
+    "recap_pager_resize": (_I, [_P, _P, ctypes.c_int32]),
     "recap_bank_copy_async": (_I, [_P, _P, _I64, _P]),
 }
 

@@ -718,6 +718,16 @@ int recap_pager_copy_time(recap_pager* pager, double* total_ms, int64_t* copies)
   return hip_status(pager_copy_time(as_pager(pager), total_ms, copies), "copy timing");
 }
 
+int recap_pager_resize(recap_pager* pager, const int64_t* field_bytes, int32_t n_fields) {
+  Pager* p = as_pager(pager);
+  REQUIRE(p != nullptr && field_bytes != nullptr, "NULL pointer");
+  REQUIRE(n_fields == pager_fields(p), "n_fields %d != the pager's %d fields", (int)n_fields,
+          pager_fields(p));
+  for (int32_t f = 0; f < n_fields; ++f)
+    REQUIRE(field_bytes[f] >= 0, "field %d has a negative size", (int)f);
+  return hip_status(pager_resize(p, field_bytes), "resize");
+}
+
 int recap_bank_copy_async(void* dst, const void* src, int64_t bytes, void* stream) {
   REQUIRE(dst && src, "NULL pointer");
   REQUIRE(bytes >= 0, "negative size");

@@ -158,5 +158,6 @@ hipError_t pager_acquire(Pager* p, int slot, hipStream_t s);
 hipError_t pager_release(Pager* p, int slot, hipStream_t s);
 hipError_t pager_finish(Pager* p);
 hipError_t pager_copy_time(Pager* p, double* total_ms, int64_t* n);
+hipError_t pager_resize(Pager* p, const int64_t* field_bytes);
 
 }  // namespace recap

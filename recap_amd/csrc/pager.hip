@@ -44,6 +44,7 @@ struct Slot {
 
 struct Key {
   std::vector<void*> host;  // pinned host fields, allocated on first use
+  std::vector<int64_t> cap; // bytes allocated per host field (>= the field's current size)
   bool stored = false;      // holds a bank written back by a refresh
   Fence written;            // last write-back into the host copy done
   Fence read;               // last prefetch out of the host copy done
@@ -57,7 +58,9 @@ struct Pager {
   hipStream_t prefetch = nullptr, writeback = nullptr;
   Fence marker;             // a point on the compute stream the write-back stream waits for
   bool timing = false;
-  std::vector<std::pair<hipEvent_t, hipEvent_t>> copies;  // timed copy batches
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> copies;  // timed copy batches not yet folded
+  double copied_ms = 0.0;   // folded batches: total milliseconds and count
+  int64_t copied_batches = 0;
   int64_t host_bytes = 0;
   int64_t counts[4] = {0, 0, 0, 0};  // stage-ins taken from a prefetch, copied; prefetches; stage-outs
 };
@@ -91,13 +94,47 @@ hipError_t wait(hipStream_t s, const Fence& f) {
     if (_e != hipSuccess) return _e;           \
   } while (0)
 
+// Pinned host fields of key k for the current field sizes: a field not yet allocated (or
+// freed by a resize that outgrew it) is allocated now.
 hipError_t ensure_host(Pager& p, Key& k) {
-  if (!k.host.empty()) return hipSuccess;
-  k.host.assign(p.bytes.size(), nullptr);
-  for (size_t f = 0; f < p.bytes.size(); ++f) {
-    HIP_TRY(hipHostMalloc(&k.host[f], (size_t)p.bytes[f], hipHostMallocDefault));
-    p.host_bytes += p.bytes[f];
+  if (k.host.empty()) {
+    k.host.assign(p.bytes.size(), nullptr);
+    k.cap.assign(p.bytes.size(), 0);
   }
+  for (size_t f = 0; f < p.bytes.size(); ++f) {
+    if (k.host[f] != nullptr) continue;
+    const int64_t n = p.bytes[f] > 0 ? p.bytes[f] : 1;
+    HIP_TRY(hipHostMalloc(&k.host[f], (size_t)n, hipHostMallocDefault));
+    k.cap[f] = n;
+    p.host_bytes += n;
+  }
+  return hipSuccess;
+}
+
+// Folds timed copy batches whose end event has completed into the running total and
+// destroys their events; with `wait`, waits for every batch first.
+hipError_t fold_copies(Pager& p, bool wait) {
+  size_t kept = 0;
+  for (size_t i = 0; i < p.copies.size(); ++i) {
+    auto& c = p.copies[i];
+    if (wait) {
+      HIP_TRY(hipEventSynchronize(c.second));
+    } else {
+      const hipError_t q = hipEventQuery(c.second);
+      if (q == hipErrorNotReady) {
+        p.copies[kept++] = c;
+        continue;
+      }
+      HIP_TRY(q);
+    }
+    float ms = 0.0f;
+    HIP_TRY(hipEventElapsedTime(&ms, c.first, c.second));
+    p.copied_ms += ms;
+    ++p.copied_batches;
+    (void)hipEventDestroy(c.first);
+    (void)hipEventDestroy(c.second);
+  }
+  p.copies.resize(kept);
   return hipSuccess;
 }
 
@@ -107,6 +144,7 @@ hipError_t copy_fields(Pager& p, const std::vector<void*>& dst, const std::vecto
                        hipMemcpyKind kind, hipStream_t s) {
   hipEvent_t t0 = nullptr, t1 = nullptr;
   if (p.timing) {
+    if (p.copies.size() >= 64) HIP_TRY(fold_copies(p, false));  // bounded event count
     HIP_TRY(hipEventCreate(&t0));
     HIP_TRY(hipEventCreate(&t1));
     HIP_TRY(hipEventRecord(t0, s));
@@ -281,15 +319,31 @@ hipError_t pager_release(Pager* p, int slot, hipStream_t s) {
 }
 
 hipError_t pager_copy_time(Pager* p, double* total_ms, int64_t* n) {
-  double total = 0.0;
-  for (auto& c : p->copies) {
-    float ms = 0.0f;
-    HIP_TRY(hipEventSynchronize(c.second));
-    HIP_TRY(hipEventElapsedTime(&ms, c.first, c.second));
-    total += ms;
+  HIP_TRY(fold_copies(*p, true));
+  *total_ms = p->copied_ms;
+  *n = p->copied_batches;
+  return hipSuccess;
+}
+
+hipError_t pager_resize(Pager* p, const int64_t* field_bytes) {
+  // Every transfer in flight reads or writes the old geometry: let them end first.
+  HIP_TRY(pager_finish(p));
+  for (size_t f = 0; f < p->bytes.size(); ++f) p->bytes[f] = field_bytes[f];
+  for (Key& k : p->keys) {
+    for (size_t f = 0; f < k.host.size(); ++f) {
+      if (k.host[f] == nullptr || k.cap[f] >= p->bytes[f]) continue;
+      HIP_TRY(hipHostFree(k.host[f]));   // outgrown: reallocated on the key's next write-back
+      p->host_bytes -= k.cap[f];
+      k.host[f] = nullptr;
+      k.cap[f] = 0;
+    }
+    k.stored = false;                    // a bank of the old geometry is no bank of the new
   }
-  *total_ms = total;
-  *n = (int64_t)p->copies.size();
+  for (Slot& s : p->slots) {
+    s.dev.clear();                       // the caller binds device fields of the new sizes
+    s.resident = -1;
+    s.prefetched = false;
+  }
   return hipSuccess;
 }
 

@@ -67,7 +67,8 @@ class HostBankOperator(Operator):
         super().__post_init__()
         self._pager: _Pager | None = None
         self._slots: list[dict[str, torch.Tensor]] = []
-        self._shape: tuple | None = None
+        self._specs: dict | None = None
+        self._turn = 0            # the slot the next call uses (slots alternate call by call)
         self._want_prefetch = True
         #: time every bank copy (set before the first call or preallocate_host)
         self.record_copies = False
@@ -92,24 +93,34 @@ class HostBankOperator(Operator):
                 "coarse_lse": ((banks, rows), torch.float32)}
 
     def _setup(self, banks: int, dim: int, device) -> None:
-        """A pager and its device slots for banks of this shape (a new shape drops the
-        banks held so far)."""
-        if self._pager is not None and self._shape == (banks, dim):
-            return
-        self._close()
+        """A pager and device slots for banks of this geometry.  The geometry is every
+        field's shape: the kernel mask [banks, tb, tb] follows the text length, which the
+        model integrations retarget per prompt (recap/models/hunyuan.py:30-39, 96-97).  A
+        new geometry drops the banks held so far; the pinned host memory is kept where it
+        is large enough (recap_pager_resize) and the slots' changed fields are reallocated."""
         specs = self._field_specs(banks, dim)
+        if self._pager is not None and self._specs == specs:
+            return
+        n_slots = 2 if self._want_prefetch else 1
         sizes = [torch.Size(s).numel() * torch.empty((), dtype=t).element_size()
                  for s, t in specs.values()]
-        n_slots = 2 if self._want_prefetch else 1
-        self._pager = _Pager(self._key(self.n_streams, 0), n_slots, sizes, self.record_copies)
-        self._slots = []
-        for slot in range(n_slots):
-            tensors = {name: torch.empty(s, dtype=t, device=device)
-                       for name, (s, t) in specs.items()}
+        if self._pager is not None and len(self._slots) == n_slots:
+            arr = (ctypes.c_int64 * len(sizes))(*sizes)
+            self._pager("resize", ctypes.cast(arr, ctypes.c_void_p), len(sizes))
+        else:
+            self._close()
+            self._pager = _Pager(self._key(self.n_streams, 0), n_slots, sizes,
+                                 self.record_copies)
+            self._slots = [{} for _ in range(n_slots)]
+        for slot, tensors in enumerate(self._slots):
+            for name, (shape, dtype) in specs.items():
+                old = tensors.get(name)
+                if old is None or tuple(old.shape) != tuple(shape) or old.dtype != dtype:
+                    tensors[name] = torch.empty(shape, dtype=dtype, device=device)
             ptrs = (ctypes.c_void_p * len(FIELDS))(*(tensors[n].data_ptr() for n in FIELDS))
             self._pager("bind", slot, ctypes.cast(ptrs, ctypes.c_void_p))
-            self._slots.append(tensors)
-        self._shape = (banks, dim)
+        self._specs = specs
+        self._turn = 0
 
     def preallocate_host(self, n_layers: int, n_banks: int, dim: int) -> int:
         """Allocate the pinned banks of the first ``n_layers`` layers (of every stream) and
@@ -137,7 +148,8 @@ class HostBankOperator(Operator):
         self._setup(b * h, dim, query.device)
         bank = self.banks[self.stream][layer_index]
         bank_key = self._key(self.stream, layer_index)
-        slot = layer_index % len(self._slots)
+        slot = self._turn
+        self._turn = (slot + 1) % len(self._slots)
         stored = self._pager.stored(bank_key)
         if self.kind == SPARSE and not stored:
             raise RuntimeError("a sparse call was requested before an exact refresh")
@@ -148,7 +160,7 @@ class HostBankOperator(Operator):
         load = stored and (self.kind == SPARSE or bank.valid)
         if load:
             self._pager("stage_in", bank_key, slot, compute)
-            self._prefetch_after(layer_index)
+            self._prefetch_next(layer_index)
         else:
             self._pager("acquire", slot, compute)
         slot_tensors = self._slots[slot]
@@ -172,27 +184,31 @@ class HostBankOperator(Operator):
                     # A refresh that loaded nothing prefetched nothing; with its bank on its
                     # way out, the next stored bank (after the stream's last layer, layer 0
                     # of the next step) can come in while the step ends.
-                    self._prefetch_after(layer_index, stored_only=True)
+                    self._prefetch_next(layer_index, stored_only=True)
         finally:
             self._pager("release", slot, compute)
             for name in FIELDS:
                 setattr(bank, name, None)
         return out
 
-    def _prefetch_after(self, layer: int, stored_only: bool = False) -> None:
-        """Bring the next layer's bank into the other slot while this layer computes; after
-        the stream's last layer the next is layer 0 of the following step.  With
-        `stored_only`, only a bank that host memory already holds."""
+    def _next_call(self, layer: int) -> tuple[int, int]:
+        """(stream, layer) of the call expected after this one: the next layer of this
+        stream; after its last layer, layer 0 of the next stream (the session runs the
+        streams of a step in turn, recap/session.py:264-308), which with one stream is the
+        next step's layer 0."""
+        if layer + 1 < len(self.layers[self.stream]):
+            return self.stream, layer + 1
+        return (self.stream + 1) % self.n_streams, 0
+
+    def _prefetch_next(self, layer: int, stored_only: bool = False) -> None:
+        """Bring the next call's bank into the slot that call will use while this layer
+        computes.  With `stored_only`, only a bank that host memory already holds."""
         if len(self._slots) < 2:
             return
-        n_layers = len(self.layers[self.stream])
-        nxt = layer + 1 if layer + 1 < n_layers else 0
-        if nxt % len(self._slots) == layer % len(self._slots):
-            return
-        key = self._key(self.stream, nxt)
+        key = self._key(*self._next_call(layer))
         if stored_only and not self._pager.stored(key):
             return
-        self._pager("prefetch", key, nxt % len(self._slots))
+        self._pager("prefetch", key, self._turn)
 
     # -- bookkeeping ---------------------------------------------------------------------
 
@@ -208,7 +224,7 @@ class HostBankOperator(Operator):
     def _close(self) -> None:
         if self._pager is not None:
             self._pager.close()
-        self._pager, self._slots, self._shape = None, [], None
+        self._pager, self._slots, self._specs, self._turn = None, [], None, 0
 
     def __del__(self):  # pragma: no cover - teardown path
         try:

@@ -223,9 +223,9 @@ def test_host_banks_multi_step_schedule_identical(cuda, layers):
     print(f"  pager counts {counts}", flush=True)
     # Every bank a layer reads after the first refresh is staged in.  With prefetch all come
     # from the prefetch stream (the first refresh, which loads nothing, prefetches the next
-    # step's layer 0 once its last layer's bank is on its way out) except, with an odd
-    # number of layers, each step's layer 0 (it shares a slot with the last layer, so it
-    # cannot be fetched during it); without prefetch all are copied on the compute stream.
+    # step's layer 0 once its last layer's bank is on its way out; the two slots alternate
+    # call by call, so with an odd number of layers too each step's layer 0 goes to the slot
+    # the last layer does not hold); without prefetch all are copied on the compute stream.
     # Each refresh writes every layer's bank back.
     steps_with_loads = len(schedule) - 1
     loads = layers * steps_with_loads
@@ -234,7 +234,7 @@ def test_host_banks_multi_step_schedule_identical(cuda, layers):
     assert counts["host-noprefetch"]["from_prefetch"] == 0
     assert counts["host-noprefetch"]["copied"] == loads
     assert counts["host"]["from_prefetch"] + counts["host"]["copied"] == loads
-    assert counts["host"]["copied"] == (0 if layers % 2 == 0 else steps_with_loads)
+    assert counts["host"]["copied"] == 0
 
 
 @pytest.mark.parametrize("name,heads", [("wan2.1-480p", 2), ("cogvideox1.5", 2),
@@ -338,3 +338,30 @@ def test_work_queue_schedule_gives_identical_outputs(cuda, monkeypatch, name):
         print(f"  balance={balance}: done", flush=True)
     assert torch.equal(outs[True][0], outs[False][0])
     assert torch.equal(outs[True][1], outs[False][1])
+
+
+def test_wan_refresh_then_four_drifting_sparse_calls_vs_oracle(cuda):
+    """The Wan2.1-480p configuration as specified: N = 32,760 video tokens (21 x 30 x 52),
+    128-dim heads, 20% density, bf16, one dense REFRESH followed by four corrected SPARSE
+    calls whose inputs drift 2% further each step (fresh N(0,1) noise per step), on 2 of the
+    12 heads (heads are independent banks).  The GPU's refinement state is handed to the
+    oracle once, after the refresh; each sparse call is then compared with the oracle's on
+    the same inputs (the state is read, never written, by a sparse call)."""
+    wl = dataclasses.replace(WORKLOADS["wan2.1-480p"], heads=2)
+    print(f"case wan2.1-480p N={wl.tokens} heads=2: REFRESH + 4 x SPARSE, 2% drift per step",
+          flush=True)
+    x = make_qkv(wl, seed=0)
+    op, perm = build(wl, layers=1)
+    ref = O.OracleOperator(wl.grid, wl.text_tokens, wl.text_first, wl.density, permutation=perm)
+    g = lambda t: t.to(cuda)  # noqa: E731
+    op.begin_step(0, REFRESH)
+    out = op.attend(0, *(g(t) for t in x))
+    ref.refresh(0, *x)
+    assert_parity(out.cpu().float(), ref.last["out_f32"], "wan refresh")
+    inject(ref, op, 0, wl)
+    for step in range(1, 5):
+        x = tuple(perturb(t, 0.02, seed=i, step=step) for i, t in enumerate(x))
+        op.begin_step(step, SPARSE)
+        got = op.attend(0, *(g(t) for t in x)).cpu()
+        ref.sparse(0, *x)
+        assert_sparse_parity(got, ref, op, *x, wl, cuda, f"wan sparse step {step}")
