@@ -412,16 +412,26 @@ def sparse_merge_attn(q: torch.Tensor, kv: PackedKV, rowmap: torch.Tensor,
 # -- stage 4 -------------------------------------------------------------------------------
 
 
+def _check_capture(dense_out, dense_lse, head_out, head_lse, go, gl, det, dl, glref, center):
+    """Argument checks shared by both capture entry points: the kernels read the head and
+    coarse outputs as 16-bit values of the dense output's type and the refinement as fp16."""
+    if not all(t.is_contiguous() for t in (dense_lse, head_out, head_lse, go, gl, det, dl)):
+        raise ValueError("capture inputs must be contiguous")
+    if head_out.dtype != dense_out.dtype or go.dtype != dense_out.dtype:
+        raise ValueError("capture: head and coarse outputs must have the dense output's dtype")
+    if det.dtype != torch.float16 or dl.dtype != torch.float32:
+        raise ValueError("capture: the refinement is fp16 values and fp32 log-masses")
+    if (glref is None) != (center is None):
+        raise ValueError("capture: validation needs both glref and center")
+
+
 def refresh_capture(dense_out: torch.Tensor, dense_lse: torch.Tensor, head_out: torch.Tensor,
                     head_lse: torch.Tensor, go: torch.Tensor, gl: torch.Tensor,
                     rowmap: torch.Tensor, geo: Geometry, det: torch.Tensor, dl: torch.Tensor,
                     glref: torch.Tensor | None = None, center: torch.Tensor | None = None):
     """Write the refinement in place; with (glref, center) return the validation pair."""
     b, h, n, d = dense_out.shape
-    if not all(t.is_contiguous() for t in (dense_lse, head_out, head_lse, go, gl, det, dl)):
-        raise ValueError("capture inputs must be contiguous")
-    if head_out.dtype != dense_out.dtype or go.dtype != dense_out.dtype:
-        raise ValueError("capture: head and coarse outputs must have the dense output's dtype")
+    _check_capture(dense_out, dense_lse, head_out, head_lse, go, gl, det, dl, glref, center)
     stats = part = None
     if glref is not None:
         npart = int(_lib.load().recap_capture_partials(b * h, d, geo.n_video))
@@ -445,8 +455,9 @@ def refresh_capture_noalloc(dense_out: torch.Tensor, dense_lse: torch.Tensor,
     (its validation partials live in a static 4 MiB device array); the caller passes the
     validation pair's output ``stats`` ([2] fp32) when validating."""
     b, h, n, d = dense_out.shape
-    if not all(t.is_contiguous() for t in (dense_lse, head_out, head_lse, go, gl, det, dl)):
-        raise ValueError("capture inputs must be contiguous")
+    _check_capture(dense_out, dense_lse, head_out, head_lse, go, gl, det, dl, glref, center)
+    if glref is not None and stats is None:
+        raise ValueError("capture: a validating call (glref given) needs the stats output")
     call("recap_refresh_capture_noalloc", dense_out.data_ptr(), dtype_code(dense_out.dtype), b,
          h, d, dense_out.stride(0), dense_out.stride(1), dense_out.stride(2),
          dense_lse.data_ptr(), head_out.data_ptr(), head_lse.data_ptr(), go.data_ptr(),
