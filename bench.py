@@ -2,15 +2,17 @@
 """Benchmark of the corrected sparse-attention call on one MI355X.
 
     python bench.py [--steps K] [--warmup W] [--workload hunyuan-720p] [--no-sequence]
+                    [--no-secondary]
 
 One "step" is one corrected SPARSE call (Operator.attend after a REFRESH) at the
 HunyuanVideo-720p shape: B=1, 24 heads x 128, 118,800 video + 256 text tokens, 128-token
 blocks, 20% density, bf16, inputs resident in HBM and drifted 2% from the refresh inputs.
 The timed region is K calls bracketed by torch.cuda.synchronize(); per-stage durations come
 from HIP events recorded on the same stream inside the timed calls.  The default run then adds
-the ten-step schedule with refinement banks paged through pinned host memory (20 layers,
-REFRESH at steps 0 and 5; ms_per_step_host_banks, copy_overlap_fraction).  Prints one JSON
-line.
+the other reference shapes (Wan2.1-480p and CogVideoX-1.5: sparse call and dense SDPA, under
+"workloads") and the ten-step schedule with refinement banks paged through pinned host memory
+(20 layers, REFRESH at steps 0 and 5; ms_per_step_host_banks, copy_overlap_fraction).  Prints
+one JSON line.
 """
 
 from __future__ import annotations
@@ -36,6 +38,8 @@ PEAK_HBM_GBS = 8000.0
 # WRITE_SIZE passes scaled by a plain copy of known size (the file records the commands).
 TRAFFIC_FILE = ROOT / "profiles" / "attention_hunyuan720p_traffic.md"
 COPY_CAL_BYTES = 1 << 30
+# The other reference shapes the default run also times (sparse call and dense SDPA).
+SECONDARY = ("wan2.1-480p", "cogvideox1.5")
 
 
 def log(msg: str) -> None:
@@ -289,8 +293,104 @@ def cpu_baseline(op, q1, k1, v1, wl, heads: int) -> dict:
         "sample": (f"oracle (torch CPU, fp32 attention) sparse call on {heads} of {wl.heads} "
                    f"heads, all {rows // 128} query blocks: {seconds:.2f} s measured, scaled "
                    f"x{wl.heads / heads:g} (heads are independent and equal in cost)"),
-        "cpu": platform.processor() or platform.machine(),
+        "cpu": cpu_model(),
     }
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or the machine type where that is absent."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def time_sparse_calls(op, q, k, v, steps: int, warmup: int) -> tuple[float, float, dict]:
+    """(mean ms per SPARSE call over ``steps`` timed calls after ``warmup`` untimed ones,
+    median ms per call, mean ms per stage) with HIP events recorded on the launch stream.
+    Python's garbage collector is paused over the timed calls: a collection pauses the host
+    for ~10-20 ms, which drains the launch queue of a short call (1.7 ms at the Wan shape)."""
+    import torch
+
+    from recap_amd import SPARSE
+
+    op.begin_step(1, SPARSE)
+    for _ in range(warmup):
+        op.attend(0, q, k, v)
+    torch.cuda.synchronize()
+    op.stage_events = {}
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    gc.collect()
+    gc.disable()
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(steps):
+        op.attend(0, q, k, v)
+    end.record()
+    torch.cuda.synchronize()
+    gc.enable()
+    ms = start.elapsed_time(end) / steps
+    stages = elapsed_stages(op.stage_events)
+    ev = op.stage_events
+    per_call = sorted(a.elapsed_time(b) for a, b in zip(ev["start"], ev["attention"]))
+    op.stage_events = None
+    return ms, per_call[len(per_call) // 2], stages
+
+
+def dense_sdpa_ms(q, k, v, reps: int) -> float:
+    """torch SDPA (the reference's EXACT path) on the same inputs, mean of ``reps``."""
+    import torch
+    import torch.nn.functional as F
+
+    F.scaled_dot_product_attention(q, k, v)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        F.scaled_dot_product_attention(q, k, v)
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / reps
+
+
+def secondary_workload(wl, steps: int, warmup: int, dense_reps: int) -> dict:
+    """One other reference shape, timed like the headline: a REFRESH, then ``steps`` SPARSE
+    calls on inputs drifted 2%, and dense SDPA on the same inputs (one JSON object)."""
+    import torch
+
+    from recap_amd import Operator, OperatorConfig, REFRESH
+    from recap_amd.layout import Layout, SparseGeometry, hilbert_permutation
+    from recap_amd.synthetic import make_qkv, perturb
+
+    dev = torch.device("cuda:0")
+    q0, k0, v0 = make_qkv(wl, seed=0, device=dev)
+    q1, k1, v1 = (perturb(x, 0.02, seed=0, step=1) for x in (q0, k0, v0))
+    layout = Layout.from_permutation(hilbert_permutation(wl.grid), text_tokens=wl.text_tokens,
+                                     text_first=wl.text_first)
+    op = Operator.build(OperatorConfig(head_density=wl.density), SparseGeometry.build(layout, 128),
+                        n_layers=1)
+    op.begin_step(0, REFRESH)
+    op.attend(0, q0, k0, v0)
+    del q0, k0, v0
+    ms, median_ms, stages = time_sparse_calls(op, q1, k1, v1, steps, warmup)
+    kept = kept_flops(op.banks[0][0].head_kernel_mask, wl.tokens, wl.dim)
+    dense = dense_sdpa_ms(q1, k1, v1, dense_reps)
+    out = {"config": {"heads": wl.heads, "head_dim": wl.dim, "tokens": wl.tokens,
+                      "text_tokens": wl.text_tokens, "text_first": wl.text_first,
+                      "density": wl.density},
+           "ms_per_call": round(ms, 4), "median_ms_per_call": round(median_ms, 4),
+           "stages_ms": {k: round(v, 4) for k, v in stages.items()},
+           "roofline_frac": round(kept / (stages["attention"] / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+           "kept_block_tflop": round(kept / 1e12, 4),
+           "dense_sdpa_ms": round(dense, 3),
+           "speedup_vs_dense_sdpa": round(dense / ms, 2),
+           "effective_tflops": round(wl.dense_flops() / 1e12 / (ms / 1e3), 2)}
+    del op
+    torch.cuda.empty_cache()
+    return out
 
 
 def main() -> int:
@@ -312,6 +412,8 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=20, help="layers of the step sequence")
     ap.add_argument("--no-sequence", action="store_true",
                     help="skip the paged step sequence of the default run")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the other reference shapes (Wan2.1, CogVideoX) of the default run")
     ap.add_argument("--refresh", type=int, default=0, metavar="K",
                     help="run only K revalidating REFRESH calls after a first one (the "
                          "selection, the capture with validation, the rerank overlap) and "
@@ -327,9 +429,8 @@ def main() -> int:
         return copy_calibration()
 
     import torch
-    import torch.nn.functional as F
 
-    from recap_amd import Operator, OperatorConfig, REFRESH, SPARSE
+    from recap_amd import Operator, OperatorConfig, REFRESH
     from recap_amd import _lib
     from recap_amd import kernels as K
     from recap_amd.layout import Layout, SparseGeometry, hilbert_permutation
@@ -363,30 +464,7 @@ def main() -> int:
     refresh_ms = (time.perf_counter() - t0) * 1e3
     log(f"[bench] first refresh (dense + selection + basis + capture) {refresh_ms:.1f} ms")
 
-    op.begin_step(1, SPARSE)
-    for _ in range(args.warmup):
-        op.attend(0, q1, k1, v1)
-    torch.cuda.synchronize()
-    log("[bench] warmup done")
-    op.stage_events = {}
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    # No garbage collection inside the timed calls: a collection pauses the host for ~10-20
-    # ms, which drains the launch queue of a short call (1.7 ms at the Wan shape).
-    gc.collect()
-    gc.disable()
-    torch.cuda.synchronize()
-    start.record()
-    for _ in range(args.steps):
-        op.attend(0, q1, k1, v1)
-    end.record()
-    torch.cuda.synchronize()
-    gc.enable()
-    ms = start.elapsed_time(end) / args.steps
-    stages = elapsed_stages(op.stage_events)
-    ev = op.stage_events
-    per_call = sorted(a.elapsed_time(b) for a, b in zip(ev["start"], ev["attention"]))
-    median_ms = per_call[len(per_call) // 2]
-    op.stage_events = None
+    ms, median_ms, stages = time_sparse_calls(op, q1, k1, v1, args.steps, args.warmup)
     log(f"[bench] sparse call {ms:.3f} ms (median {median_ms:.3f}); stages {stages}")
 
     # Stage-1 selection (REFRESH-only in the reference) on the same inputs, timed alone so
@@ -446,15 +524,7 @@ def main() -> int:
         },
     }
     if not args.profile:
-        F.scaled_dot_product_attention(q1, k1, v1)
-        torch.cuda.synchronize()
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record()
-        for _ in range(args.dense_reps):
-            F.scaled_dot_product_attention(q1, k1, v1)
-        e.record()
-        torch.cuda.synchronize()
-        dense_ms = s.elapsed_time(e) / args.dense_reps
+        dense_ms = dense_sdpa_ms(q1, k1, v1, args.dense_reps)
         result["dense_sdpa_ms"] = round(dense_ms, 3)
         result["speedup_vs_dense_sdpa"] = round(dense_ms / ms, 2)
         gemm = gemm_peak_tflops()
@@ -468,6 +538,22 @@ def main() -> int:
             result["cpu_baseline"] = cpu_baseline(op, q1, k1, v1, wl, args.cpu_heads)
             log(f"[bench] CPU baseline {result['cpu_baseline']['value']} ms/call "
                 f"({result['cpu_baseline']['sample']})")
+        if not args.no_secondary:
+            # The other reference shapes: sparse call and dense SDPA only (no sequence, no
+            # CPU leg); the headline above is unchanged.
+            del op, q0, k0, v0, kv
+            op = q0 = k0 = v0 = kv = None
+            torch.cuda.empty_cache()
+            result["workloads"] = {}
+            for name in SECONDARY:
+                if name == wl.name:
+                    continue
+                log(f"[bench] secondary workload {name} ...")
+                sec = secondary_workload(WORKLOADS[name], args.steps, args.warmup,
+                                         args.dense_reps)
+                result["workloads"][name] = sec
+                log(f"[bench] {name}: {sec['ms_per_call']} ms/call, attention frac "
+                    f"{sec['roofline_frac']}, {sec['speedup_vs_dense_sdpa']}x dense SDPA")
         if not args.no_sequence:
             # The ten-step schedule with paged refinement banks: REFRESH at steps 0 and 5,
             # SPARSE otherwise, 3% drift, args.layers layers; paged vs resident banks.
