@@ -182,8 +182,8 @@ class HostBankOperator(Operator):
                 self._pager("stage_out", bank_key, slot, compute)
                 if not load:
                     # A refresh that loaded nothing prefetched nothing; with its bank on its
-                    # way out, the next stored bank (after the stream's last layer, layer 0
-                    # of the next step) can come in while the step ends.
+                    # way out, the next call's bank, if host memory holds one, can come in
+                    # while this call ends.
                     self._prefetch_next(layer_index, stored_only=True)
         finally:
             self._pager("release", slot, compute)
