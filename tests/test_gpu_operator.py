@@ -113,27 +113,62 @@ def test_fp16_and_batched_calls_vs_oracle(cuda, name, dtype, batch):
 @pytest.mark.parametrize("name", list(SMALL))
 def test_sparse_vs_oracle_with_independent_state(cuda, name):
     """End to end with separately computed refinement states.  The coarse tail's gate
-    [s^2 qsq.w <= theta^2] is discontinuous and D = (of - ratio oh)/(1 - ratio) - go
-    amplifies last-bit differences of the bf16 dense/head outputs, so a few elements may
-    move by more than a bf16 ulp; the bulk must still agree."""
+    [s^2 qsq.w <= theta^2] is discontinuous, the closure basis of each side comes from its
+    own eigensolver (rotations within nearly equal eigenvalues move qsq), and
+    D = (of - ratio oh)/(1 - ratio) - go amplifies last-bit differences of the bf16
+    dense/head outputs, so a few elements may move by more than a bf16 ulp.  The same call
+    on the oracle given the GPU's state (basis, partition, D, DL, gl_ref) must meet the
+    strict bar, and every element of the GPU's output must lie within the bar plus the
+    oracle's own change between its state and the GPU's: the differences beyond the bar
+    come from the state alone (whose capture the refresh tests check on identical inputs),
+    and they are no larger than the oracle's sensitivity to it.  Cosine >= 0.999 overall."""
     wl = SMALL[name]
     q, k, v = make_qkv(wl, seed=0)
     op, perm = build(wl)
-    ref = O.OracleOperator(wl.grid, wl.text_tokens, wl.text_first, wl.density, permutation=perm)
+    new_ref = lambda: O.OracleOperator(wl.grid, wl.text_tokens, wl.text_first,  # noqa: E731
+                                       wl.density, permutation=perm)
+    ref = new_ref()
     op.begin_step(0, REFRESH)
     op.attend(0, q.to(cuda), k.to(cuda), v.to(cuda))
     ref.refresh(0, q, k, v)
     q1, k1, v1 = (perturb(x, 0.02, seed=1, step=1) for x in (q, k, v))
     op.begin_step(1, SPARSE)
-    out = op.attend(0, q1.to(cuda), k1.to(cuda), v1.to(cuda)).cpu().float()
+    out_dev = op.attend(0, q1.to(cuda), k1.to(cuda), v1.to(cuda))
+    out = out_dev.cpu().float()
     ref.sparse(0, q1, k1, v1)
     want = ref.last["out_f32"]
     m, c = metrics(out, want)
-    frac = float(((out - want.to(torch.bfloat16).float()).abs()
-                  > parity_tolerance(want)).float().mean())
+    beyond = lambda x, r: (x - r.to(torch.bfloat16).float()).abs() > parity_tolerance(r)  # noqa: E731
+    far = beyond(out, want)
+    frac = float(far.float().mean())
     print(f"[independent {name}] max_abs={m:.3e} cos={c:.6f} frac-beyond-tolerance={frac:.2e}",
           flush=True)
-    assert c >= 0.999 and frac <= 1e-3 and m < 0.25
+    assert c >= 0.999
+    # The oracle given the GPU's state: strict parity.
+    ref_g = new_ref()
+    inject(ref_g, op, 0, wl)
+    ref_g.sparse(0, q1, k1, v1)
+    assert_sparse_parity(out_dev, ref_g, op, q1, k1, v1, wl, cuda, f"given the GPU state {name}")
+    # The state's own effect on the oracle: its output with its own state against its output
+    # with the GPU's (basis alone, then the whole state).
+    state = op.layers[0][0]
+    ref_b = new_ref()
+    ref_b.refresh(0, q, k, v)
+    ref_b.layers[0].basis = state.basis.cpu().float()
+    ref_b.sparse(0, q1, k1, v1)
+    by_state = beyond(ref_g.last["out_f32"].float(), want)
+    by_basis = beyond(ref_b.last["out_f32"].float(), want)
+    print(f"  oracle with the GPU's state vs its own: {int(by_state.sum())} elements beyond the "
+          f"bar (GPU vs oracle: {int(far.sum())}; both: {int((far & by_state).sum())}); "
+          f"with the GPU's basis only: {int(by_basis.sum())}", flush=True)
+    # |out - own| <= |out - given| + |given - own|, each side rounded as the outputs are
+    given = ref_g.last["out_f32"].float()
+    r16 = lambda x: x.to(torch.bfloat16).double()  # noqa: E731
+    gap = (r16(given) - r16(want)).abs()
+    excess = (out.double() - r16(want)).abs() - (parity_tolerance(given) + gap)
+    print(f"  worst against the bar plus the state's effect: {float(excess.max()):+.3e}",
+          flush=True)
+    assert float(excess.max()) <= 0
 
 
 def test_alpha_override_knob_vs_oracle(cuda):
