@@ -676,13 +676,13 @@ class OracleOperator:
         scale = 1.0 / math.sqrt(d)
         rows = (self.n_video // self.block) * self.block
         ql, kl, vl = self._banks(q), self._banks(k), self._banks(v)
-        oh, lh = block_sparse_attention(ql, kl, vl, state.kmask, scale, self.block)
-        oh = cast(oh, dtype)
+        oh32, lh = block_sparse_attention(ql, kl, vl, state.kmask, scale, self.block)
+        oh = cast(oh32, dtype)
         ctx = self._context(state, ql, kl, vl, dtype)
         go, gl = self._coarse(ql, ctx, state.partition, dtype, rows)
         center = drift_center(gl, state.glref)
         merged32 = sparse_merge(oh, lh, go, gl, state.det, state.dl, rows, state.glref, center,
                                 alpha_override)
-        self.last = {"ctx": ctx, "oh": oh, "lh": lh, "go": go, "gl": gl, "center": center,
-                     "out_f32": restore(merged32, self.inv).reshape(b, h, n, d)}
+        self.last = {"ctx": ctx, "oh": oh, "oh_f32": oh32, "lh": lh, "go": go, "gl": gl,
+                     "center": center, "out_f32": restore(merged32, self.inv).reshape(b, h, n, d)}
         return restore(cast(merged32, dtype), self.inv).reshape(b, h, n, d)
