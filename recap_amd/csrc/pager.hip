@@ -112,30 +112,32 @@ hipError_t ensure_host(Pager& p, Key& k) {
 }
 
 // Folds timed copy batches whose end event has completed into the running total and
-// destroys their events; with `wait`, waits for every batch first.
+// destroys their events; with `wait`, waits for every batch first.  On an error the batch
+// that raised it and the later ones are kept.
 hipError_t fold_copies(Pager& p, bool wait) {
-  size_t kept = 0;
-  for (size_t i = 0; i < p.copies.size(); ++i) {
-    auto& c = p.copies[i];
-    if (wait) {
-      HIP_TRY(hipEventSynchronize(c.second));
-    } else {
-      const hipError_t q = hipEventQuery(c.second);
-      if (q == hipErrorNotReady) {
-        p.copies[kept++] = c;
-        continue;
-      }
-      HIP_TRY(q);
+  size_t kept = 0, i = 0;
+  hipError_t err = hipSuccess;
+  for (; i < p.copies.size(); ++i) {
+    const auto c = p.copies[i];
+    hipError_t e = wait ? hipEventSynchronize(c.second) : hipEventQuery(c.second);
+    if (!wait && e == hipErrorNotReady) {
+      p.copies[kept++] = c;
+      continue;
     }
     float ms = 0.0f;
-    HIP_TRY(hipEventElapsedTime(&ms, c.first, c.second));
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, c.first, c.second);
+    if (e != hipSuccess) {
+      err = e;
+      break;
+    }
     p.copied_ms += ms;
     ++p.copied_batches;
     (void)hipEventDestroy(c.first);
     (void)hipEventDestroy(c.second);
   }
+  for (; i < p.copies.size(); ++i) p.copies[kept++] = p.copies[i];
   p.copies.resize(kept);
-  return hipSuccess;
+  return err;
 }
 
 // Copies every field between `dst` and `src` on `s`, bracketed by timing events when the
@@ -143,19 +145,25 @@ hipError_t fold_copies(Pager& p, bool wait) {
 hipError_t copy_fields(Pager& p, const std::vector<void*>& dst, const std::vector<void*>& src,
                        hipMemcpyKind kind, hipStream_t s) {
   hipEvent_t t0 = nullptr, t1 = nullptr;
+  hipError_t e = hipSuccess;
   if (p.timing) {
     if (p.copies.size() >= 64) HIP_TRY(fold_copies(p, false));  // bounded event count
-    HIP_TRY(hipEventCreate(&t0));
-    HIP_TRY(hipEventCreate(&t1));
-    HIP_TRY(hipEventRecord(t0, s));
+    e = hipEventCreate(&t0);
+    if (e == hipSuccess) e = hipEventCreate(&t1);
+    if (e == hipSuccess) e = hipEventRecord(t0, s);
   }
-  for (size_t f = 0; f < p.bytes.size(); ++f)
-    if (p.bytes[f] > 0) HIP_TRY(hipMemcpyAsync(dst[f], src[f], (size_t)p.bytes[f], kind, s));
+  for (size_t f = 0; f < p.bytes.size() && e == hipSuccess; ++f)
+    if (p.bytes[f] > 0) e = hipMemcpyAsync(dst[f], src[f], (size_t)p.bytes[f], kind, s);
   if (p.timing) {
-    HIP_TRY(hipEventRecord(t1, s));
-    p.copies.emplace_back(t0, t1);
+    if (e == hipSuccess) e = hipEventRecord(t1, s);
+    if (e == hipSuccess) {
+      p.copies.emplace_back(t0, t1);
+    } else {  // a batch that did not complete its records is not timed
+      if (t0) (void)hipEventDestroy(t0);
+      if (t1) (void)hipEventDestroy(t1);
+    }
   }
-  return hipSuccess;
+  return e;
 }
 
 }  // namespace

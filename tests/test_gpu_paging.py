@@ -161,3 +161,28 @@ def test_host_banks_with_two_streams(cuda, layers):
     loads = 2 * layers * (len(schedule) - 1)
     assert counts["written_back"] == 2 * layers * schedule.count(REFRESH)
     assert counts["copied"] == 0 and counts["from_prefetch"] == loads
+
+
+def test_timed_copies_fold_over_a_long_run(cuda):
+    """With every bank copy timed (record_copies), a run of more than 64 copy batches keeps
+    a bounded number of timing events (finished batches are folded into a running total as
+    new ones start) and copy_time() reports every batch: stage-ins copied on the compute
+    stream, prefetches and write-backs, with a positive total."""
+    wl = SMALL["tiny"]
+    geometry = _geometry(wl)
+    layers = 2
+    resident, paged = _pair(wl, geometry, layers=layers)
+    paged.record_copies = True
+    q, k, v = make_qkv(wl, seed=9, device=cuda)
+    steps = 40
+    for step in range(steps):
+        kind = REFRESH if step % 10 == 0 else SPARSE
+        inputs = tuple(perturb(x, 0.02, seed=j, step=step) for j, x in enumerate((q, k, v)))
+        _run_step((resident, paged), step, kind, [(0, layer, inputs) for layer in range(layers)])
+    paged.finish()
+    counts = paged.pager_counts()
+    ms, batches = paged.copy_time()
+    print(f"  counts {counts}, timed batches {batches}, {ms:.3f} ms", flush=True)
+    assert batches == counts["copied"] + counts["prefetches"] + counts["written_back"]
+    assert batches > 64 and ms > 0
+    assert paged.copy_time() == (ms, batches)   # folded batches are counted once
