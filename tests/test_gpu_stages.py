@@ -31,7 +31,12 @@ LONG = {"long-row-d64": Workload("long-row-d64", 1, 64, (4, 35, 1006), 0, False,
                                  torch.bfloat16),
         # 71 video blocks, the last one ragged (40 tokens)
         "mid-row-d128": Workload("mid-row-d128", 2, 128, (3, 25, 120), 0, False, 0.2,
-                                 torch.bfloat16)}
+                                 torch.bfloat16),
+        # The largest shape the kernels take: 2,048 kernel blocks (the attention kernel's
+        # kept list holds at most 2,048): 36 x 75 x 97 = 261,900 video tokens (2,047 blocks,
+        # the last one 12 tokens, shared with the text) + 200 text tokens = 262,100.
+        "max-blocks-d128": Workload("max-blocks-d128", 1, 128, (36, 75, 97), 200, False, 0.2,
+                                    torch.bfloat16)}
 
 
 def _setup(name, heads, cuda, seed=0, dtype=None, k_factors=None):
@@ -337,7 +342,77 @@ def test_coarse_tail_score_jumps(cuda, name):
     _check_coarse_tail(cuda, name, 4, k_factors=(1.0, 3.0, 0.5, 6.0, 1.5, 10.0, 0.75, 4.0))
 
 
-def _check_coarse_tail(cuda, name, rank, k_factors=None):
+def _rows_of(blocks, n):
+    return torch.cat([torch.arange(128 * i, min(128 * (i + 1), n)) for i in blocks])
+
+
+def test_max_blocks_stage1_and_attention(cuda):
+    """The largest shape the kernels take: 2,048 kernel blocks, one head of d = 128, the text
+    sharing the ragged last video block.  Stage 1 bit-exact in full (2,047 x 2,047 block
+    scores); the head and dense attention against the oracle on sampled query blocks: the
+    first, a middle one, the last full video block, the ragged shared block and the text
+    block (both dense rows: the text block walks all 2,048 key tiles, the kept list's
+    capacity)."""
+    wl, (q, k, v), (qg, kg, vg), rowmap, fwd, geo = _setup("max-blocks-d128", None, cuda)
+    assert geo.tb == 2048 and geo.nb == 2047
+    scale = scale_for(wl.dim)
+    kv = K.kv_pack(kg, vg, rowmap, geo)
+    ql, kl, vl = (banks_view(x, fwd) for x in (q, k, v))
+    part, kmask = K.pool_select(qg, kv.k_means, rowmap, geo, wl.density, scale)
+    part_ref = O.head_partition(ql, kl, scale, wl.density, wl.video_tokens)
+    kmask_ref = O.kernel_block_mask(part_ref, wl.tokens, wl.video_tokens)
+    assert torch.equal(part.cpu(), part_ref) and torch.equal(kmask.cpu(), kmask_ref)
+    print(f"  partition and kernel mask bit-exact; kept per video row "
+          f"{int(part_ref[0, 0].sum())}, text row {int(kmask_ref[0, -1].sum())}", flush=True)
+    blocks = [0, geo.nb // 2, geo.ds - 1, geo.nb - 1, geo.tb - 1]
+    rows = _rows_of(blocks, wl.tokens)
+    out, lse = K.block_sparse_attn(qg, kv, rowmap, kmask, geo, scale)
+    ref, ref_lse = O.block_sparse_attention(ql, kl, vl, kmask_ref, scale, query_blocks=blocks)
+    assert_parity(out.cpu().float()[:, rows], ref[:, rows], "head, 2,048 blocks")
+    m, _ = metrics(lse.cpu()[:, rows], ref_lse[:, rows])
+    assert m < 2e-3, m
+    dense, dlse = K.dense_attn(qg, kv, rowmap, scale)
+    dblocks = [0, geo.tb - 1]
+    drows = _rows_of(dblocks, wl.tokens)
+    dref, dref_lse = O.dense_attention(ql, kl, vl, scale, query_blocks=dblocks)
+    native = torch.as_tensor(fwd, dtype=torch.long)[drows]
+    got = dense.cpu().float().reshape(1, wl.tokens, wl.dim)[:, native]
+    assert_parity(got, dref[:, drows], "dense, 2,048 blocks")
+    m, _ = metrics(dlse.cpu().reshape(1, wl.tokens)[:, native], dref_lse[:, drows])
+    assert m < 2e-3, m
+
+
+def test_max_blocks_coarse_tail_sampled(cuda):
+    """The coarse kernel at 2,048 kernel blocks (rows of ~1,640 omitted blocks, 52 tiles)
+    against the oracle on the first, a middle and the last full video block."""
+    _check_coarse_tail(cuda, "max-blocks-d128", 4, blocks=[0, 1023, 2045])
+
+
+def test_max_blocks_refresh_then_sparse_reproduces_dense(cuda):
+    """The whole operator at 2,048 kernel blocks: the refresh's dense output against torch
+    SDPA, and a sparse call on the refresh's own inputs reproduces it (the refinement holds
+    exactly what the head and coarse tail miss)."""
+    from recap_amd import REFRESH, SPARSE, Operator, OperatorConfig
+    from recap_amd.layout import SparseGeometry
+
+    wl = LONG["max-blocks-d128"]
+    perm = hilbert_permutation(wl.grid)
+    layout = Layout.from_permutation(perm, text_tokens=wl.text_tokens, text_first=wl.text_first)
+    op = Operator.build(OperatorConfig(head_density=wl.density),
+                        SparseGeometry.build(layout, 128), n_layers=1)
+    q, k, v = make_qkv(wl, seed=0, device=cuda)
+    op.begin_step(0, REFRESH)
+    dense = op.attend(0, q, k, v)
+    ref = torch.nn.functional.scaled_dot_product_attention(q.float(), k.float(), v.float())
+    assert_parity(dense.float(), ref, "dense vs sdpa, 2,048 blocks")
+    op.begin_step(1, SPARSE)
+    sparse = op.attend(0, q, k, v)
+    assert_parity(sparse.float(), dense.float(), "refresh -> sparse == dense, 2,048 blocks")
+
+
+def _check_coarse_tail(cuda, name, rank, k_factors=None, blocks=None):
+    """The coarse kernel against the oracle on the same closure statistics, on every row or
+    (``blocks``) on the rows of those query blocks."""
     wl, (q, k, v), (qg, kg, vg), rowmap, fwd, geo = _setup(name, None, cuda,
                                                           k_factors=k_factors)
     scale = scale_for(wl.dim)
@@ -356,8 +431,10 @@ def _check_coarse_tail(cuda, name, rank, k_factors=None):
     qsq = O.rotated_query_square(qv, basis, torch.bfloat16)
     drift = O.value_drift(qv, cvk, scale, torch.bfloat16)
     go_ref, gl_ref = O.coarse_tail(ql, qsq, drift, km_ref, vm_ref, w, counts, part, scale, 2.0,
-                                   wl.video_tokens, torch.bfloat16)
+                                   wl.video_tokens, torch.bfloat16, query_blocks=blocks)
     rows = geo.rows
+    sel = (torch.arange(rows) if blocks is None else
+           torch.cat([torch.arange(128 * i, min(128 * (i + 1), rows)) for i in blocks]))
     qt = K.basis_tables(basis.to(cuda), cvk.to(cuda), kv.dtype, query=True, cvk_table=True)
     wt, kbar, vbar = K.coarse_tables(var.to(cuda), kv, rank)
     assert wt.shape[-1] == (16 if 1 <= rank <= 13 and kv.dtype == torch.bfloat16 else wl.dim)
@@ -370,10 +447,11 @@ def _check_coarse_tail(cuda, name, rank, k_factors=None):
               "rank": rank}
     glref = torch.randn(kl.shape[0], rows, generator=torch.Generator().manual_seed(3)).to(cuda)
     go, gl, dpart = K.coarse_tail(qg, rowmap, part.to(cuda), geo, tables, scale, 2.0, glref)
-    assert_parity(go.cpu().float(), go_ref[:, :rows], f"coarse {name}")
-    fin = torch.isfinite(gl_ref[:, :rows])
-    assert torch.equal(torch.isfinite(gl.cpu()), fin)
-    err = torch.where(fin, (gl.cpu() - gl_ref[:, :rows]).abs(), torch.zeros(()))
+    assert_parity(go.cpu().float()[:, sel], go_ref[:, sel], f"coarse {name}")
+    gl_s = gl.cpu()[:, sel]
+    fin = torch.isfinite(gl_ref[:, sel])
+    assert torch.equal(torch.isfinite(gl_s), fin)
+    err = torch.where(fin, (gl_s - gl_ref[:, sel]).abs(), torch.zeros(()))
     bad = err > 2e-3
     if bad.any():
         # The gate fl(s^2 qsq.w) <= theta^2 is discontinuous: the other decision moves a
@@ -384,7 +462,7 @@ def _check_coarse_tail(cuda, name, rank, k_factors=None):
         # (b) qsq itself: the reference's U^T q is a bf16 GEMM whose fp32 accumulation order
         #     is open (recap/sparse/closure.py:84-86), and one element of it can round to the
         #     neighbouring bf16 value; qsq from an MFMA-accumulated GEMM on the GPU.
-        blocks = sorted({int(r) // 128 for r in torch.nonzero(bad.any(0)).flatten()})
+        bad_blocks = sorted({int(sel[r]) // 128 for r in torch.nonzero(bad.any(0)).flatten()})
         ub = O.cast(basis, torch.bfloat16).to(torch.bfloat16).to(cuda)
         rot = torch.stack([qv[i].to(torch.bfloat16).to(cuda) @ ub[i].contiguous()
                            for i in range(qv.shape[0])]).float().cpu()
@@ -395,8 +473,9 @@ def _check_coarse_tail(cuda, name, rank, k_factors=None):
         best = torch.full_like(err, math.inf)
         for qsq_alt, th in alternates:
             _, gl_alt = O.coarse_tail(ql, qsq_alt, drift, km_ref, vm_ref, w, counts, part, scale,
-                                      th, wl.video_tokens, torch.bfloat16, query_blocks=blocks)
-            best = torch.minimum(best, (gl.cpu() - gl_alt[:, :rows]).abs())
+                                      th, wl.video_tokens, torch.bfloat16,
+                                      query_blocks=bad_blocks)
+            best = torch.minimum(best, (gl_s - gl_alt[:, sel]).abs())
         print(f"  gl: {int(bad.sum())} rows over 2e-3 (max {float(err.max()):.3e}); against "
               f"the gate and qsq alternates max {float(best[bad].max()):.3e}", flush=True)
         assert float(best[bad].max()) < 2e-3, float(best[bad].max())
