@@ -109,6 +109,9 @@ def test_argument_validation_before_launch():
     with pytest.raises(ValueError, match="rank"):
         _lib.call("recap_coarse_tail", 16, _lib.RECAP_BF16, 1, 1, 64, 0, 0, 64, 16, 16, 16, 16,
                   16, 16, 16, 256, 256, 0.125, 2.0, 65, None, 16, 16, 16, None)
+    with pytest.raises(ValueError, match="video blocks"):   # the coarse kernel's row limit
+        _lib.call("recap_coarse_tail", 16, _lib.RECAP_BF16, 1, 1, 64, 0, 0, 64, 16, 16, 16, 16,
+                  16, 16, 16, 4097 * 128, 4097 * 128, 0.125, 2.0, 4, None, 16, 16, 16, None)
     width = _lib.load().recap_coarse_w_width
     assert width(_lib.RECAP_BF16, 128, 4) == 16 and width(_lib.RECAP_BF16, 64, 13) == 16
     assert width(_lib.RECAP_BF16, 128, 0) == 128 and width(_lib.RECAP_BF16, 128, 14) == 128
