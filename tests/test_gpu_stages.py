@@ -6,7 +6,6 @@ cosine >= 0.999; fp32 statistics within the tolerance stated per test."""
 
 import math
 
-import numpy as np
 import pytest
 import torch
 

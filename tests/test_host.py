@@ -1,7 +1,6 @@
 """Host-side checks that need no GPU: the C ABI library loads and exports every symbol
 the header declares, host-only entry points, argument validation, config and layout."""
 
-import ctypes
 import json
 import re
 from pathlib import Path

@@ -7,7 +7,6 @@ from __future__ import annotations
 import math
 
 import numpy as np
-import pytest
 import torch
 from hypothesis import HealthCheck, given, settings
 from hypothesis import strategies as st
