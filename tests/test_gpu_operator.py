@@ -400,3 +400,48 @@ def test_wan_refresh_then_four_drifting_sparse_calls_vs_oracle(cuda):
         got = op.attend(0, *(g(t) for t in x)).cpu()
         ref.sparse(0, *x)
         assert_sparse_parity(got, ref, op, *x, wl, cuda, f"wan sparse step {step}")
+
+
+def test_two_host_threads_on_two_streams_match_serial(cuda):
+    """The library keeps no mutable global state on the call path: two host threads, each
+    with its own stream and operator, run a REFRESH and three SPARSE calls at the same time
+    (three rounds); every output equals the same sequence run alone, bit for bit."""
+    import threading
+
+    wl = SMALL["text-last-d128"]
+    schedule = [REFRESH, SPARSE, SPARSE, SPARSE]
+
+    def run(seed, stream):
+        with torch.cuda.stream(stream):
+            op, _ = build(wl, layers=1)
+            q, k, v = make_qkv(wl, seed=seed, device=cuda)
+            outs = []
+            for step, kind in enumerate(schedule):
+                x = tuple(perturb(t, 0.02, seed=j, step=step) for j, t in enumerate((q, k, v)))
+                op.begin_step(step, kind)
+                outs.append(op.attend(0, *x).clone())
+            stream.synchronize()
+        return [o.cpu() for o in outs]
+
+    streams = [torch.cuda.Stream() for _ in range(2)]
+    serial = [run(10 + i, streams[i]) for i in range(2)]
+    for rnd in range(3):
+        results, errors = [None, None], []
+
+        def worker(i):
+            try:
+                results[i] = run(10 + i, streams[i])
+            except Exception as exc:  # re-raised below, in the test's thread
+                errors.append(exc)
+
+        threads = [threading.Thread(target=worker, args=(i,)) for i in range(2)]
+        for t in threads:
+            t.start()
+        for t in threads:
+            t.join()
+        if errors:
+            raise errors[0]
+        for i in range(2):
+            for step, (a, b) in enumerate(zip(serial[i], results[i])):
+                assert torch.equal(a, b), (rnd, i, step)
+        print(f"  round {rnd}: both threads equal their serial runs", flush=True)

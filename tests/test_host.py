@@ -293,3 +293,27 @@ def test_attention_branches_over_disjoint_keys_merge_to_the_full_softmax():
     empty = AttentionBranch(torch.zeros_like(a.output), torch.full_like(a.lse, float("-inf")))
     same = a.merge(empty)
     torch.testing.assert_close(same.output, a.output.float().double(), atol=1e-6, rtol=1e-6)
+
+
+def test_last_error_is_per_thread():
+    """recap_last_error() reports the calling thread's own last failure: a failing call in
+    one thread leaves another thread's message untouched (callers on distinct host threads
+    and streams do not see each other's errors)."""
+    import threading
+
+    lib = _lib.load()
+    lib.recap_symmetric_eigen(16, 2, 0, 16, 16, None)   # matrix order 0: this thread's error
+    mine = lib.recap_last_error().decode()
+    assert "matrix order" in mine
+    seen = {}
+
+    def other():
+        seen["before"] = lib.recap_last_error().decode()
+        lib.recap_topk_blocks(16, 1, 10, 11, 0, 16, None)    # keep > blocks
+        seen["after"] = lib.recap_last_error().decode()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert "matrix order" not in seen["before"] and "keep" in seen["after"]
+    assert lib.recap_last_error().decode() == mine
