@@ -14,7 +14,12 @@
  *    ordered video tokens first, then the text tokens (recap/sparse/layout.py:44-61).
  *  - Block size is 128; dim is 64 or 128; dtype is RECAP_BF16 or RECAP_F16.
  *  - Derived sizes: nb = ceil(n_video/128) video blocks, tb = ceil(n_tokens/128) kernel
- *    blocks, R = floor(n_video/128)*128 refined rows.
+ *    blocks, R = floor(n_video/128)*128 refined rows.  Limits: tb <= 2048 for the attention
+ *    entry points, nb <= 4096 for selection and the coarse tail (RECAP_EINVAL beyond).
+ *  - Calls on distinct streams from distinct host threads may run concurrently when they
+ *    use distinct buffers (work queues included); the library holds no mutable state on
+ *    those paths.  The exceptions are recap_refresh_capture_noalloc (one static scratch
+ *    array per GPU) and a pager, which one host thread drives.
  */
 #ifndef RECAP_HIP_H
 #define RECAP_HIP_H

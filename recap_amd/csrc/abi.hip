@@ -259,6 +259,9 @@ int recap_pool_select(const void* q, int dtype, int64_t batch, int64_t heads, in
           (double)scale);
   REQUIRE(batch >= 1 && heads >= 1, "bad batch/heads");
   const Geom g = geometry(n_tokens, n_video);
+  // every check of the four stages is made here, before the first of them launches
+  CHECK(check_common(dtype, dim));
+  REQUIRE(g.nb <= 4096, "too many video blocks (%lld > 4096)", (long long)g.nb);
   const int64_t banks = batch * heads;
   const int64_t need = recap_pool_select_workspace_size(banks, g.nb, dim);
   REQUIRE(need > 0 && workspace_bytes >= need, "workspace of %lld bytes, need %lld",

@@ -127,6 +127,9 @@ def test_argument_validation_before_launch():
     with pytest.raises(ValueError, match="density"):
         _lib.call("recap_pool_select", 16, _lib.RECAP_BF16, 1, 2, 64, 0, 0, 64, 16, 512, 512,
                   16, 0.125, 1.5, 16, need, 16, 16, None)
+    with pytest.raises(ValueError, match="video blocks"):   # before any of its four stages
+        _lib.call("recap_pool_select", 16, _lib.RECAP_BF16, 1, 2, 64, 0, 0, 64, 16,
+                  4097 * 128, 4097 * 128, 16, 0.125, 0.25, 16, 1 << 40, 16, 16, None)
 
 
 def test_workspace_queries():
