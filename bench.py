@@ -246,6 +246,55 @@ def refresh_calls(wl, count: int) -> dict:
             round(error, 6)}
 
 
+def band_sweep(wl, keeps=(4, 16, 48, 96, 186, 280), reps: int = 10) -> dict:
+    """The merge kernel's time against the kept tiles per row, on the workload's inputs with
+    synthetic band masks (each video query block keeps the ``keep`` key blocks centred on
+    itself; the kernel-mask expansion adds the text rows and columns): the work items stay
+    fixed while the tile steps grow, which separates the per-step cost from the per-item
+    one.  The drift weight is fixed at 0.5 (no drift inputs)."""
+    import torch
+
+    from recap_amd import kernels as K
+    from recap_amd.layout import Layout, hilbert_permutation
+    from recap_amd.synthetic import make_qkv
+
+    dev = torch.device("cuda:0")
+    q, k, v = make_qkv(wl, seed=0, device=dev)
+    layout = Layout.from_permutation(hilbert_permutation(wl.grid), text_tokens=wl.text_tokens,
+                                     text_first=wl.text_first)
+    rowmap = layout.rowmap(dev)
+    geo = K.Geometry(wl.tokens, wl.video_tokens)
+    kv = K.kv_pack(k, v, rowmap, geo)
+    banks, nb, rows, d = wl.heads, geo.nb, geo.rows, wl.dim
+    g = torch.Generator(device=dev).manual_seed(1)
+    go = torch.randn(banks, rows, d, device=dev, generator=g).to(q.dtype)
+    gl = torch.randn(banks, rows, device=dev, generator=g)
+    det = (0.1 * torch.randn(banks, rows, d, device=dev, generator=g)).to(torch.float16)
+    dl = torch.randn(banks, rows, device=dev, generator=g)
+    idx = torch.arange(nb, device=dev)
+    out = []
+    for keep in keeps:
+        lo = (idx - keep // 2).clamp(0, max(nb - keep, 0))
+        part = (idx[None, :] >= lo[:, None]) & (idx[None, :] < lo[:, None] + keep)
+        kmask = K.kernel_block_mask(part[None].expand(banks, nb, nb).contiguous(), geo)
+        steps = int(kmask.sum())
+        call = lambda: K.sparse_merge_attn(q, kv, rowmap, kmask, geo, d ** -0.5, go, gl,  # noqa: E731
+                                           det, dl, None, None, alpha_override=0.5)
+        for _ in range(3):
+            call()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            call()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        log(f"[band] keep {keep}: {steps} tile steps, {ms:.3f} ms, {ms * 1e6 / steps:.2f} ns/step")
+        out.append({"keep": keep, "tile_steps": steps, "ms": round(ms, 4),
+                    "ns_per_step": round(ms * 1e6 / steps, 3)})
+    return {"band_sweep": wl.name, "items": banks * geo.tb, "points": out}
+
+
 def cpu_baseline(op, q1, k1, v1, wl, heads: int) -> dict:
     """The oracle's sparse call on the host for ``heads`` of the heads (all query blocks),
     timed with the operator's refinement state; heads are independent and cost the same,
@@ -414,6 +463,9 @@ def main() -> int:
                     help="skip the paged step sequence of the default run")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the other reference shapes (Wan2.1, CogVideoX) of the default run")
+    ap.add_argument("--band-sweep", action="store_true",
+                    help="run only the merge kernel with synthetic band masks of 4-280 kept "
+                         "blocks per row (per-step against per-item cost) and print its JSON")
     ap.add_argument("--refresh", type=int, default=0, metavar="K",
                     help="run only K revalidating REFRESH calls after a first one (the "
                          "selection, the capture with validation, the rerank overlap) and "
@@ -444,6 +496,9 @@ def main() -> int:
         return 0
     if args.refresh > 0:
         print(json.dumps(refresh_calls(wl, args.refresh)), flush=True)
+        return 0
+    if args.band_sweep:
+        print(json.dumps(band_sweep(wl)), flush=True)
         return 0
     log(f"[bench] workload {wl.name}: heads={wl.heads} d={wl.dim} N={wl.tokens}")
     q0, k0, v0 = make_qkv(wl, seed=0, device=dev)
