@@ -449,7 +449,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="hunyuan-720p")
     ap.add_argument("--dense-reps", type=int, default=3)
-    ap.add_argument("--cpu-heads", type=int, default=2,
+    ap.add_argument("--cpu-heads", type=int, default=3,
                     help="heads of the CPU baseline sample (0 = skip)")
     ap.add_argument("--profile", action="store_true",
                     help="only the sparse calls (no dense comparator, no CPU baseline)")
