@@ -126,15 +126,16 @@ def scale_for(d: int) -> float:
     return 1.0 / math.sqrt(d)
 
 
-def gate_alternates(ref, q, wl, rel: float = 1e-5, dtype=torch.bfloat16, alpha_override=None):
+def gate_alternates(ref, q, wl, rel: float = 1e-5, dtype=torch.bfloat16, alpha_override=None,
+                    layer: int = 0):
     """The oracle's last sparse output with the coarse tail's gate threshold theta^2 moved
     up and down by ``rel`` (relative), for the rows whose gate decision lies within ``rel``
     of the threshold (``O.gate_margin``).  Two fp32 summation orders of qsq.w (the
     reference's own ``tl.dot`` leaves the order open, recap/kernels/coarse_tail.py:139-140)
     may decide such a (row, block) pair either way; moving the threshold across it gives
     the other decision.  Returns ``(borderline [B, H, N, 1] bool, [out_up, out_down])``,
-    outputs fp32 in native order.  Needs ``ref.sparse(0, q, ...)`` to have just run."""
-    last, state = ref.last, ref.layers[0]
+    outputs fp32 in native order.  Needs ``ref.sparse(layer, q, ...)`` to have just run."""
+    last, state = ref.last, ref.layers[layer]
     ctx = last["ctx"]
     b, h, n, d = q.shape
     scale = 1.0 / math.sqrt(d)
@@ -188,7 +189,7 @@ def neighbour16(x: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
 
 
 def head_alternate(ref, op, q, k, v, device, dtype=torch.bfloat16, alpha_override=None,
-                   need=None):
+                   need=None, layer: int = 0):
     """The oracle's last sparse output with its head branch rounded the other way at the
     elements where a kernel that rounds P may legitimately do so.
 
@@ -210,8 +211,8 @@ def head_alternate(ref, op, q, k, v, device, dtype=torch.bfloat16, alpha_overrid
     native)``."""
     from recap_amd import kernels as K
 
-    last, state = ref.last, ref.layers[0]
-    bank = op.banks[0][0]
+    last, state = ref.last, ref.layers[layer]
+    bank = op.banks[0][layer]
     b, h, n, d = q.shape
     qg, kg, vg = (x.to(device) for x in (q, k, v))
     geo = op._geometry(qg)
@@ -258,6 +259,17 @@ def head_alternate(ref, op, q, k, v, device, dtype=torch.bfloat16, alpha_overrid
     return flip_native, out_alt
 
 
+def inject(ref, op, layer_index, wl):
+    """Give the oracle the GPU operator's refinement state (basis, partition, D, DL, gl_ref)
+    of one layer (stream 0)."""
+    bank, layer = op.banks[0][layer_index], op.layers[0][layer_index]
+    nb = bank.partition.shape[-1]
+    ref.load_state(layer_index, basis=layer.basis.cpu(),
+                   partition=bank.partition.reshape(-1, nb, nb).cpu(),
+                   det=bank.value.cpu(), dl=bank.log_mass.cpu(), glref=bank.coarse_lse.cpu(),
+                   n_tokens=wl.tokens)
+
+
 def elements_within(got, ref, dtype=torch.bfloat16, max_abs=2e-2) -> torch.Tensor:
     """Elementwise: within ``parity_tolerance`` of ``ref`` rounded to ``dtype``."""
     g, r = got.double().cpu(), ref.cpu().to(dtype).double()
@@ -265,18 +277,20 @@ def elements_within(got, ref, dtype=torch.bfloat16, max_abs=2e-2) -> torch.Tenso
 
 
 def assert_sparse_parity(got, ref, op, q, k, v, wl, device, what, dtype=torch.bfloat16,
-                         alpha_override=None, cos=0.999):
-    """A corrected sparse output (layer 0 of ``op``; ``ref.sparse`` on the same inputs and
-    state has just run) against the oracle: every element within ``parity_tolerance`` of the
+                         alpha_override=None, cos=0.999, layer: int = 0):
+    """A corrected sparse output (``layer`` of ``op``, stream 0; ``ref.sparse`` on the same
+    inputs and state has just run) against the oracle: every element within ``parity_tolerance`` of the
     oracle's output, or of the oracle with one legitimately ambiguous rounding decided the
     other way -- the coarse tail's gate for a (row, block) pair within 1e-5 of theta^2
     (``gate_alternates``) or the head branch's bf16 rounding (``head_alternate``) -- and
     cosine >= ``cos``.  No element is left unchecked; the counts are printed."""
     got = got.double().cpu()
     want = ref.last["out_f32"]
-    borderline, gate_alt = gate_alternates(ref, q, wl, dtype=dtype, alpha_override=alpha_override)
+    borderline, gate_alt = gate_alternates(ref, q, wl, dtype=dtype, alpha_override=alpha_override,
+                                           layer=layer)
     ok = elements_within(got, want, dtype)
-    flip, head_alt = head_alternate(ref, op, q, k, v, device, dtype, alpha_override, need=~ok)
+    flip, head_alt = head_alternate(ref, op, q, k, v, device, dtype, alpha_override, need=~ok,
+                                    layer=layer)
     by_gate = borderline & (elements_within(got, gate_alt[0], dtype)
                             | elements_within(got, gate_alt[1], dtype))
     by_head = flip & elements_within(got, head_alt, dtype)

@@ -8,7 +8,8 @@ import pytest
 import torch
 
 import oracle as O
-from gpu_util import (SMALL, assert_parity, assert_sparse_parity, metrics, parity_tolerance)
+from gpu_util import (SMALL, assert_parity, assert_sparse_parity, inject, metrics,
+                      parity_tolerance)
 from recap_amd import HostBankOperator, Operator, OperatorConfig, REFRESH, SPARSE
 from recap_amd.layout import Layout, SparseGeometry, hilbert_permutation
 from recap_amd.synthetic import WORKLOADS, make_qkv, perturb
@@ -26,16 +27,6 @@ def build(wl, *, chunks=1, host_banks=False, prefetch=True, layers=2):
     if host_banks:
         op.set_prefetch(prefetch)
     return op, perm
-
-
-def inject(ref, op, layer_index, wl):
-    """Give the oracle the GPU operator's refinement state (basis, partition, D, DL, gl_ref)."""
-    bank, layer = op.banks[0][layer_index], op.layers[0][layer_index]
-    nb = bank.partition.shape[-1]
-    ref.load_state(layer_index, basis=layer.basis.cpu(),
-                   partition=bank.partition.reshape(-1, nb, nb).cpu(),
-                   det=bank.value.cpu(), dl=bank.log_mass.cpu(), glref=bank.coarse_lse.cpu(),
-                   n_tokens=wl.tokens)
 
 
 @pytest.mark.parametrize("name", list(SMALL))
