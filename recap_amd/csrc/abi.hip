@@ -380,16 +380,18 @@ int recap_coarse_tail(const void* q, int dtype, int64_t batch, int64_t heads, in
   CHECK(check_common(dtype, dim));
   CHECK(check_tokens(n_tokens, n_video));
   CHECK(check_qkv("q", q, batch, heads, stride_b, stride_h, stride_n));
-  REQUIRE(rowmap && partition && kbar && vbar && w && u_t && cvk_t && go && gl, "NULL pointer");
+  REQUIRE(rowmap && partition && kbar && vbar && w && u_t && cvk_t, "NULL pointer");
   REQUIRE(std::isfinite(scale) && scale > 0.0f, "scale must be positive and finite");
   REQUIRE(theta >= 0.0f, "theta must be non-negative");
   REQUIRE(rank >= 0 && rank <= dim, "rank %lld outside [0, dim]", (long long)rank);
-  REQUIRE(aligned16(kbar) && aligned16(vbar) && aligned16(w) && aligned16(u_t) && aligned16(cvk_t) && aligned16(go),
+  REQUIRE(aligned16(kbar) && aligned16(vbar) && aligned16(w) && aligned16(u_t) && aligned16(cvk_t),
           "tables must be 16-byte aligned");
-  REQUIRE(glref == nullptr || drift_partial != nullptr, "glref needs drift_partial");
   const Geom g = geometry(n_tokens, n_video);
   REQUIRE(g.nb <= 4096, "too many video blocks (%lld > 4096)", (long long)g.nb);
+  // No full video block: no refined rows, nothing to write (go, gl may be empty buffers).
   if (g.rows == 0) return RECAP_OK;
+  REQUIRE(go && gl && aligned16(go), "go and gl must be non-NULL, go 16-byte aligned");
+  REQUIRE(glref == nullptr || drift_partial != nullptr, "glref needs drift_partial");
   CoarseArgs a{};
   a.q = static_cast<const uint16_t*>(q); a.sB = stride_b; a.sH = stride_h; a.sN = stride_n;
   a.rowmap = rowmap; a.partition = partition;
@@ -405,9 +407,11 @@ int recap_coarse_tail(const void* q, int dtype, int64_t batch, int64_t heads, in
 
 int recap_drift_center(const float* drift_partial, int64_t banks, int64_t n_video, float* center,
                        void* stream) {
-  REQUIRE(drift_partial && center, "NULL pointer");
-  REQUIRE(banks >= 1 && n_video >= kBlock, "bad banks/n_video");
+  REQUIRE(center, "NULL pointer");
+  REQUIRE(banks >= 1 && n_video >= 1, "bad banks/n_video");
   const int64_t rows = (n_video / kBlock) * kBlock;
+  if (rows == 0) return RECAP_OK;  // no refined rows: no centre is used
+  REQUIRE(drift_partial, "NULL pointer");
   return hip_status(run_drift_center(drift_partial, (int)banks, (int)(rows / kBlock), (int)rows, center,
                                      as_stream(stream)),
                     "drift_center launch");
@@ -530,7 +534,14 @@ int64_t recap_capture_partials(int64_t banks, int64_t dim, int64_t n_video) {
   return banks * ((n_video / kBlock) * kBlock / rpb);
 }
 
-// Arguments of a refresh capture, validated; false when there is nothing to do (R = 0).
+// With no refined rows (R = 0) a validation sums nothing: both sums are zero, written by a
+// fill kernel (a caller may capture the call into a graph).
+static int zero_stats(float* stats, hipStream_t s) {
+  return hip_status(run_zero_words(reinterpret_cast<unsigned*>(stats), 2, s), "stats reset");
+}
+
+// Arguments of a refresh capture, validated; `work` is false when there is nothing to do
+// (R = 0).
 static int capture_args(const void* dense_out, int dtype, int64_t batch, int64_t heads,
                         int64_t dim, int64_t out_stride_b, int64_t out_stride_h,
                         int64_t out_stride_n, const float* dense_lse, const void* head_out,
@@ -541,11 +552,15 @@ static int capture_args(const void* dense_out, int dtype, int64_t batch, int64_t
   CHECK(check_common(dtype, dim));
   CHECK(check_tokens(n_tokens, n_video));
   CHECK(check_qkv("dense_out", dense_out, batch, heads, out_stride_b, out_stride_h, out_stride_n));
-  REQUIRE(dense_lse && head_out && head_lse && go && gl && rowmap && det && dl, "NULL pointer");
-  REQUIRE(aligned16(head_out) && aligned16(go) && aligned16(det), "16-byte alignment");
-  REQUIRE(glref == nullptr || (center && stats), "validation needs center and stats");
+  REQUIRE(dense_lse && head_out && head_lse && rowmap, "NULL pointer");
+  REQUIRE(aligned16(head_out), "16-byte alignment");
+  REQUIRE(glref == nullptr || stats, "validation needs stats");
   const Geom g = geometry(n_tokens, n_video);
   work = g.rows > 0;
+  if (!work) return RECAP_OK;  // no refined rows: go, gl, det, dl may be empty buffers
+  REQUIRE(go && gl && det && dl, "NULL pointer");
+  REQUIRE(aligned16(go) && aligned16(det), "16-byte alignment");
+  REQUIRE(glref == nullptr || center, "validation needs center");
   a.of = static_cast<const uint16_t*>(dense_out);
   a.osB = out_stride_b; a.osH = out_stride_h; a.osN = out_stride_n;
   a.lf = dense_lse; a.oh = static_cast<const uint16_t*>(head_out); a.lh = head_lse;
@@ -573,7 +588,7 @@ int recap_refresh_capture(const void* dense_out, int dtype, int64_t batch, int64
   REQUIRE(!validate || stat_partial, "validation needs stat_partial");
   REQUIRE(!validate || (reinterpret_cast<uintptr_t>(stat_partial) & 7) == 0,
           "stat_partial must be 8-byte aligned");
-  if (!work) return RECAP_OK;
+  if (!work) return validate ? zero_stats(stats, as_stream(stream)) : RECAP_OK;
   a.stat_part = stat_partial;
   int blocks = 0;
   hipStream_t s = as_stream(stream);
@@ -604,7 +619,7 @@ int recap_refresh_capture_noalloc(const void* dense_out, int dtype, int64_t batc
             "recap_refresh_capture with a caller workspace",
             (long long)pairs, (long long)kCaptureScratchPairs);
   }
-  if (!work) return RECAP_OK;
+  if (!work) return validate ? zero_stats(stats, as_stream(stream)) : RECAP_OK;
   float* scratch = nullptr;
   if (validate) CHECK(hip_status(capture_scratch_pointer(&scratch), "static scratch lookup"));
   a.stat_part = scratch;

@@ -12,7 +12,7 @@ from gpu_util import (SMALL, assert_parity, assert_sparse_parity, inject, metric
                       parity_tolerance)
 from recap_amd import HostBankOperator, Operator, OperatorConfig, REFRESH, SPARSE
 from recap_amd.layout import Layout, SparseGeometry, hilbert_permutation
-from recap_amd.synthetic import WORKLOADS, make_qkv, perturb
+from recap_amd.synthetic import WORKLOADS, Workload, make_qkv, perturb
 
 pytestmark = pytest.mark.gpu
 
@@ -436,3 +436,57 @@ def test_two_host_threads_on_two_streams_match_serial(cuda):
             for step, (a, b) in enumerate(zip(serial[i], results[i])):
                 assert torch.equal(a, b), (rnd, i, step)
         print(f"  round {rnd}: both threads equal their serial runs", flush=True)
+
+
+@pytest.mark.parametrize("grid,text,text_first", [
+    ((1, 5, 20), 60, False),    # 100 video tokens: no full block, no refined rows
+    ((1, 4, 25), 30, True),     # the same, text first
+    ((1, 1, 128), 10, False),   # one full video block: it keeps every block, no tail
+    ((1, 2, 100), 0, False),    # two blocks, the ragged last one forced: no tail either
+])
+def test_short_videos_vs_oracle(cuda, grid, text, text_first):
+    """Videos of at most two blocks, against the oracle (the GPU's state handed over after
+    the refresh).  Under one full block there are no refined rows: the refresh is the dense
+    call and the sparse call the head.  When a query block keeps every video block its
+    coarse tail is empty (log-mass -inf, also in the refresh's gl_ref) and the reference's
+    merge makes its rows NaN: the drift weight exp(-|gl - gl_ref - c|) takes -inf - (-inf)
+    (recap/kernels/detail_cache.py:267-284).  The same elements are NaN here; every other
+    element meets the bar."""
+    wl = Workload("short", 2, 64, grid, text, text_first, 0.25, torch.bfloat16)
+    print(f"case grid={grid} text={text} text_first={text_first}", flush=True)
+    q, k, v = make_qkv(wl, seed=0)
+    op, perm = build(wl, layers=1)
+    ref = O.OracleOperator(wl.grid, wl.text_tokens, wl.text_first, wl.density, permutation=perm)
+    op.begin_step(0, REFRESH)
+    out = op.attend(0, q.to(cuda), k.to(cuda), v.to(cuda)).cpu().float()
+    ref.refresh(0, q, k, v)
+    assert_parity(out, ref.last["out_f32"], f"refresh {grid}")
+    inject(ref, op, 0, wl)
+    q1, k1, v1 = (perturb(x, 0.02, seed=1, step=1) for x in (q, k, v))
+    op.begin_step(1, SPARSE)
+    got = op.attend(0, q1.to(cuda), k1.to(cuda), v1.to(cuda)).cpu().float()
+    ref.sparse(0, q1, k1, v1)
+    want = ref.last["out_f32"]
+    nan = want.isnan()
+    print(f"  NaN elements: oracle {int(nan.sum())}, here {int(got.isnan().sum())}", flush=True)
+    assert torch.equal(got.isnan(), nan)
+    if not bool(nan.all()):
+        assert_parity(got.nan_to_num(), want.nan_to_num(), f"sparse {grid}")
+    if wl.video_tokens < 128:
+        assert not bool(nan.any())
+    # A revalidating refresh: with no refined rows both sums are zero (error inf, as the
+    # reference's drain gives for a zero denominator); with the empty tails both are NaN.
+    q2, k2, v2 = (perturb(x, 0.03, seed=1, step=2) for x in (q, k, v))
+    op.begin_step(2, REFRESH)
+    out = op.attend(0, q2.to(cuda), k2.to(cuda), v2.to(cuda)).cpu().float()
+    ref.refresh(0, q2, k2, v2)
+    assert_parity(out, ref.last["out_f32"], f"refresh-2 {grid}")
+    age, error = op.drain_validation()
+    num, den = (float(x) for x in ref.layers[0].pending_stats)
+    want_err = math.sqrt(num / den) if den > 0 else float("inf")
+    print(f"  validation error here {error} oracle {want_err}", flush=True)
+    assert age == 2
+    if math.isnan(want_err) or math.isinf(want_err):
+        assert (math.isnan(error) and math.isnan(want_err)) or error == want_err
+    else:
+        assert abs(error - want_err) < 2e-3

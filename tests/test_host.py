@@ -320,3 +320,29 @@ def test_last_error_is_per_thread():
     t.join()
     assert "matrix order" not in seen["before"] and "keep" in seen["after"]
     assert lib.recap_last_error().decode() == mine
+
+
+def test_no_refined_rows_needs_no_row_buffers():
+    """A video of fewer than 128 tokens has no refined rows (R = 0): the coarse tail, the
+    capture (without validation) and the drift centre accept empty (NULL) row buffers and
+    return before any launch, as the reference handles empty tensors; with R > 0 the same
+    NULL buffers are rejected."""
+    lib = _lib.load()
+    # recap_coarse_tail(q, dtype, B, H, d, strides, rowmap, partition, kbar, vbar, w, u_t,
+    # cvk_t, n_tokens, n_video, scale, theta, rank, glref, go, gl, drift_partial, stream)
+    args = lambda n: (16, _lib.RECAP_BF16, 1, 2, 64, 0, 0, 64, 16, 16, 16, 16, 16, 16, 16,  # noqa: E731
+                      n + 40, n, 0.125, 2.0, 4, None, None, None, None, None)
+    assert lib.recap_coarse_tail(*args(100)) == _lib.RECAP_OK
+    with pytest.raises(ValueError, match="go and gl"):
+        _lib.call("recap_coarse_tail", *args(300))
+    # recap_refresh_capture(dense_out, dtype, B, H, d, out strides, dense_lse, head_out,
+    # head_lse, go, gl, rowmap, n_tokens, n_video, det, dl, glref, center, stat_partial,
+    # stats, stream)
+    cap = lambda n: (16, _lib.RECAP_BF16, 1, 2, 64, 0, 0, 64, 16, 16, 16, None, None, 16,  # noqa: E731
+                     n + 40, n, None, None, None, None, None, None, None)
+    assert lib.recap_refresh_capture(*cap(100)) == _lib.RECAP_OK
+    with pytest.raises(ValueError, match="NULL"):
+        _lib.call("recap_refresh_capture", *cap(300))
+    assert lib.recap_drift_center(None, 2, 100, 16, None) == _lib.RECAP_OK
+    with pytest.raises(ValueError, match="NULL"):
+        _lib.call("recap_drift_center", None, 2, 300, 16, None)
