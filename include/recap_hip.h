@@ -17,8 +17,8 @@
  *    blocks, R = floor(n_video/128)*128 refined rows.  With R = 0 (fewer than 128 video
  *    tokens) the buffers sized by R may be NULL: recap_coarse_tail and recap_drift_center
  *    do nothing, a capture writes stats = (0, 0) when validating, and the merge keeps the
- *    head.  Limits: tb <= 2048 for the attention
- *    entry points, nb <= 4096 for selection and the coarse tail (RECAP_EINVAL beyond).
+ *    head.  Limits: tb <= 2048 for the attention entry points, nb <= 4096 for selection
+ *    and the coarse tail (RECAP_EINVAL beyond).
  *  - Calls on distinct streams from distinct host threads may run concurrently when they
  *    use distinct buffers (work queues included); the library holds no mutable state on
  *    those paths.  The exceptions are recap_refresh_capture_noalloc (one static scratch
