@@ -16,9 +16,9 @@
  *  - Derived sizes: nb = ceil(n_video/128) video blocks, tb = ceil(n_tokens/128) kernel
  *    blocks, R = floor(n_video/128)*128 refined rows.  With R = 0 (fewer than 128 video
  *    tokens) the buffers sized by R may be NULL: recap_coarse_tail and recap_drift_center
- *    do nothing, a capture writes stats = (0, 0) when validating, and the merge keeps the
- *    head.  Limits: tb <= 2048 for the attention entry points, nb <= 4096 for selection
- *    and the coarse tail (RECAP_EINVAL beyond).
+ *    do nothing, a capture writes stats = (0, 0) when stats is non-NULL, and the merge
+ *    keeps the head.  Limits: tb <= 2048 for the attention entry points, nb <= 4096 for
+ *    selection and the coarse tail (RECAP_EINVAL beyond).
  *  - Calls on distinct streams from distinct host threads may run concurrently when they
  *    use distinct buffers (work queues included); the library holds no mutable state on
  *    those paths.  The exceptions are recap_refresh_capture_noalloc (one static scratch
@@ -295,7 +295,8 @@ int recap_refresh_capture_noalloc(const void* dense_out, int dtype, int64_t batc
  * through n_slots device slots.  A bank is n_fields byte ranges of the given sizes (the
  * operator pages value fp16 [banks, R, dim], log_mass fp32 [banks, R], partition
  * [B, H, nb, nb], kernel mask [banks, tb, tb] and the drift reference fp32 [banks, R]); a
- * slot's device fields are owned by the caller and bound once.  The pager owns a prefetch
+ * slot's device fields are owned by the caller and bound once (a field of zero bytes may
+ * be bound as NULL).  The pager owns a prefetch
  * and a write-back stream (non-blocking, default priority) and the events that fence every
  * reuse of a slot and of a key's host copy.  RECAP_PAGER_TIMING times every copy batch
  * (recap_pager_copy_time).  One pager is driven by one host thread; destroying it waits

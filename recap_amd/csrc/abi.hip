@@ -535,7 +535,8 @@ int64_t recap_capture_partials(int64_t banks, int64_t dim, int64_t n_video) {
 }
 
 // With no refined rows (R = 0) a validation sums nothing: both sums are zero, written by a
-// fill kernel (a caller may capture the call into a graph).
+// fill kernel (a caller may capture the call into a graph).  The R-sized glref is then an
+// empty buffer, possibly NULL, so a non-NULL `stats` alone asks for the sums.
 static int zero_stats(float* stats, hipStream_t s) {
   return hip_status(run_zero_words(reinterpret_cast<unsigned*>(stats), 2, s), "stats reset");
 }
@@ -588,7 +589,7 @@ int recap_refresh_capture(const void* dense_out, int dtype, int64_t batch, int64
   REQUIRE(!validate || stat_partial, "validation needs stat_partial");
   REQUIRE(!validate || (reinterpret_cast<uintptr_t>(stat_partial) & 7) == 0,
           "stat_partial must be 8-byte aligned");
-  if (!work) return validate ? zero_stats(stats, as_stream(stream)) : RECAP_OK;
+  if (!work) return stats ? zero_stats(stats, as_stream(stream)) : RECAP_OK;
   a.stat_part = stat_partial;
   int blocks = 0;
   hipStream_t s = as_stream(stream);
@@ -619,7 +620,7 @@ int recap_refresh_capture_noalloc(const void* dense_out, int dtype, int64_t batc
             "recap_refresh_capture with a caller workspace",
             (long long)pairs, (long long)kCaptureScratchPairs);
   }
-  if (!work) return validate ? zero_stats(stats, as_stream(stream)) : RECAP_OK;
+  if (!work) return stats ? zero_stats(stats, as_stream(stream)) : RECAP_OK;
   float* scratch = nullptr;
   if (validate) CHECK(hip_status(capture_scratch_pointer(&scratch), "static scratch lookup"));
   a.stat_part = scratch;
@@ -670,8 +671,9 @@ int recap_pager_bind(recap_pager* pager, int32_t slot, void* const* device_field
   REQUIRE(p != nullptr && device_fields != nullptr, "NULL pointer");
   REQUIRE(slot >= 0 && slot < pager_slots(p), "slot %d outside 0..%d", (int)slot,
           pager_slots(p) - 1);
-  for (int f = 0; f < pager_fields(p); ++f)
-    REQUIRE(device_fields[f] != nullptr, "device field %d is NULL", f);
+  for (int f = 0; f < pager_fields(p); ++f)   // an empty field may have no memory
+    REQUIRE(device_fields[f] != nullptr || pager_field_bytes(p, f) == 0,
+            "device field %d is NULL", f);
   pager_bind(p, slot, device_fields);
   return RECAP_OK;
 }

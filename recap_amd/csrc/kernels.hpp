@@ -145,6 +145,7 @@ void pager_destroy(Pager* p);
 int pager_slots(const Pager* p);
 int64_t pager_keys(const Pager* p);
 int pager_fields(const Pager* p);
+int64_t pager_field_bytes(const Pager* p, int field);
 bool pager_bound(const Pager* p, int slot);
 bool pager_stored(const Pager* p, int64_t key);
 int64_t pager_host_bytes(const Pager* p);

@@ -235,6 +235,7 @@ void pager_destroy(Pager* p) {
 int pager_slots(const Pager* p) { return (int)p->slots.size(); }
 int64_t pager_keys(const Pager* p) { return (int64_t)p->keys.size(); }
 int pager_fields(const Pager* p) { return (int)p->bytes.size(); }
+int64_t pager_field_bytes(const Pager* p, int field) { return p->bytes[(size_t)field]; }
 bool pager_bound(const Pager* p, int slot) { return !p->slots[(size_t)slot].dev.empty(); }
 bool pager_stored(const Pager* p, int64_t key) { return p->keys[(size_t)key].stored; }
 int64_t pager_host_bytes(const Pager* p) { return p->host_bytes; }

@@ -5,6 +5,7 @@ with bank_chunks = 4 (the HunyuanVideo profiles), and two streams (Wan's two CFG
 step, recap/models/wan.py:22).  In each, paged outputs equal resident ones bit for bit."""
 
 import dataclasses
+import math
 
 import pytest
 import torch
@@ -186,3 +187,27 @@ def test_timed_copies_fold_over_a_long_run(cuda):
     assert batches == counts["copied"] + counts["prefetches"] + counts["written_back"]
     assert batches > 64 and ms > 0
     assert paged.copy_time() == (ms, batches)   # folded batches are counted once
+
+
+def test_host_banks_with_no_refined_rows(cuda):
+    """A video of fewer than 128 tokens (100 video + 60 text): the paged bank's refinement
+    fields are empty (zero bytes) and the kernel mask is the only field with data; paged ==
+    resident over REFRESH / SPARSE / REFRESH / SPARSE on two layers, validations included."""
+    from recap_amd.synthetic import Workload
+
+    wl = Workload("short", 2, 64, (1, 5, 20), 60, False, 0.25, torch.bfloat16)
+    geometry = _geometry(wl)
+    layers = 2
+    resident, paged = _pair(wl, geometry, layers=layers)
+    q, k, v = make_qkv(wl, seed=3, device=cuda)
+    schedule = [REFRESH, SPARSE, REFRESH, SPARSE]
+    for step, kind in enumerate(schedule):
+        inputs = tuple(perturb(x, 0.02, seed=j, step=step) for j, x in enumerate((q, k, v)))
+        stats = _run_step((resident, paged), step, kind,
+                          [(0, layer, inputs) for layer in range(layers)])
+        if stats is not None and stats[0] is not None:
+            assert stats[0] == stats[1], (step, stats)
+            assert math.isinf(stats[0][1])
+        print(f"  step {step} {kind}: paged == resident", flush=True)
+    paged.finish()
+    print(f"  pager counts {paged.pager_counts()}", flush=True)
