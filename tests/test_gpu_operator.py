@@ -490,3 +490,31 @@ def test_short_videos_vs_oracle(cuda, grid, text, text_first):
         assert (math.isnan(error) and math.isnan(want_err)) or error == want_err
     else:
         assert abs(error - want_err) < 2e-3
+
+
+@pytest.mark.parametrize("grid,text,text_first,dim", [
+    ((2, 16, 16), 100, False, 128),   # 512 video tokens: four whole blocks, text after
+    ((2, 16, 16), 226, True, 64),     # the same video, text first (CogVideoX-like)
+    ((3, 16, 24), 256, False, 128),   # 1,152 tokens: nine whole blocks, two text blocks
+])
+def test_video_in_whole_blocks_with_text_vs_oracle(cuda, grid, text, text_first, dim):
+    """A video of whole 128-token blocks next to text: no ragged block is shared between
+    video and text, so the text rows and columns stand alone.  REFRESH then SPARSE against
+    the oracle, on the GPU's state, under the strict bar."""
+    wl = Workload("whole", 2, dim, grid, text, text_first, 0.25, torch.bfloat16)
+    print(f"case grid={grid} text={text} text_first={text_first} d={dim}", flush=True)
+    q, k, v = make_qkv(wl, seed=2)
+    op, perm = build(wl, layers=1)
+    ref = O.OracleOperator(wl.grid, wl.text_tokens, wl.text_first, wl.density, permutation=perm)
+    op.begin_step(0, REFRESH)
+    out = op.attend(0, q.to(cuda), k.to(cuda), v.to(cuda))
+    ref.refresh(0, q, k, v)
+    assert_parity(out.cpu().float(), ref.last["out_f32"], f"refresh {grid}")
+    assert torch.equal(op.banks[0][0].partition.cpu().reshape(ref.layers[0].partition.shape),
+                       ref.layers[0].partition)
+    inject(ref, op, 0, wl)
+    q1, k1, v1 = (perturb(x, 0.02, seed=1, step=1) for x in (q, k, v))
+    op.begin_step(1, SPARSE)
+    out = op.attend(0, q1.to(cuda), k1.to(cuda), v1.to(cuda))
+    ref.sparse(0, q1, k1, v1)
+    assert_sparse_parity(out, ref, op, q1, k1, v1, wl, cuda, f"sparse {grid}")
