@@ -518,3 +518,31 @@ def test_video_in_whole_blocks_with_text_vs_oracle(cuda, grid, text, text_first,
     out = op.attend(0, q1.to(cuda), k1.to(cuda), v1.to(cuda))
     ref.sparse(0, q1, k1, v1)
     assert_sparse_parity(out, ref, op, q1, k1, v1, wl, cuda, f"sparse {grid}")
+
+
+@pytest.mark.parametrize("density,q_scale", [(0.03, 1.0), (0.9, 1.0), (0.25, 4.0)])
+def test_density_extremes_and_peaky_queries_vs_oracle(cuda, density, q_scale):
+    """The tiny shape (32 blocks) at the selection's extremes -- one kept block per query
+    block (31 in the coarse tail), and 29 kept (3 in the tail) -- and with queries scaled
+    by 4, so the softmax over keys and over block means is peaked (log-masses spread over
+    tens of units).  REFRESH then SPARSE against the oracle on the GPU's state, strict bar."""
+    wl = dataclasses.replace(SMALL["tiny"], density=density)
+    print(f"case density={density} q_scale={q_scale}", flush=True)
+    q, k, v = make_qkv(wl, seed=5)
+    if q_scale != 1.0:
+        q = (q.float() * q_scale).to(q.dtype)
+    op, perm = build(wl, layers=1)
+    ref = O.OracleOperator(wl.grid, wl.text_tokens, wl.text_first, wl.density, permutation=perm)
+    op.begin_step(0, REFRESH)
+    out = op.attend(0, q.to(cuda), k.to(cuda), v.to(cuda))
+    ref.refresh(0, q, k, v)
+    assert_parity(out.cpu().float(), ref.last["out_f32"], f"refresh d={density} s={q_scale}")
+    part = ref.layers[0].partition
+    assert torch.equal(op.banks[0][0].partition.cpu().reshape(part.shape), part)
+    print(f"  kept per query block {int(part[0, 0].sum())} of {part.shape[-1]}", flush=True)
+    inject(ref, op, 0, wl)
+    q1, k1, v1 = (perturb(x, 0.02, seed=1, step=1) for x in (q, k, v))
+    op.begin_step(1, SPARSE)
+    out = op.attend(0, q1.to(cuda), k1.to(cuda), v1.to(cuda))
+    ref.sparse(0, q1, k1, v1)
+    assert_sparse_parity(out, ref, op, q1, k1, v1, wl, cuda, f"sparse d={density} s={q_scale}")
