@@ -546,3 +546,34 @@ def test_density_extremes_and_peaky_queries_vs_oracle(cuda, density, q_scale):
     out = op.attend(0, q1.to(cuda), k1.to(cuda), v1.to(cuda))
     ref.sparse(0, q1, k1, v1)
     assert_sparse_parity(out, ref, op, q1, k1, v1, wl, cuda, f"sparse d={density} s={q_scale}")
+
+
+@pytest.mark.parametrize("name,theta,rank", [
+    ("text-last-d128", 0.5, 0),      # tight gate, no leading closure directions
+    ("text-last-d128", 8.0, 13),     # loose gate, the largest folded rank
+    ("video-ragged-d128", 2.0, 20),  # rank past the folded form: the full w table
+    ("text-first-ragged", 2.0, 64),  # rank = dim at d = 64
+])
+def test_gate_theta_and_closure_rank_vs_oracle(cuda, name, theta, rank):
+    """The operator's coarse-tail knobs (closure_gate_theta, closure_rank of
+    recap/config.py:56-80) away from their defaults: REFRESH then SPARSE against the oracle
+    built with the same knobs, on the GPU's state, under the strict bar."""
+    wl = SMALL[name]
+    print(f"case {name} theta={theta} rank={rank}", flush=True)
+    q, k, v = make_qkv(wl, seed=6)
+    perm = hilbert_permutation(wl.grid)
+    layout = Layout.from_permutation(perm, text_tokens=wl.text_tokens, text_first=wl.text_first)
+    cfg = OperatorConfig(head_density=wl.density, closure_gate_theta=theta, closure_rank=rank)
+    op = Operator.build(cfg, SparseGeometry.build(layout, 128), n_layers=1)
+    ref = O.OracleOperator(wl.grid, wl.text_tokens, wl.text_first, wl.density, theta=theta,
+                           rank=rank, permutation=perm)
+    op.begin_step(0, REFRESH)
+    out = op.attend(0, q.to(cuda), k.to(cuda), v.to(cuda))
+    ref.refresh(0, q, k, v)
+    assert_parity(out.cpu().float(), ref.last["out_f32"], f"refresh {name} {theta} {rank}")
+    inject(ref, op, 0, wl)
+    q1, k1, v1 = (perturb(x, 0.02, seed=1, step=1) for x in (q, k, v))
+    op.begin_step(1, SPARSE)
+    out = op.attend(0, q1.to(cuda), k1.to(cuda), v1.to(cuda))
+    ref.sparse(0, q1, k1, v1)
+    assert_sparse_parity(out, ref, op, q1, k1, v1, wl, cuda, f"sparse {name} {theta} {rank}")
