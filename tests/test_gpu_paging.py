@@ -211,3 +211,28 @@ def test_host_banks_with_no_refined_rows(cuda):
         print(f"  step {step} {kind}: paged == resident", flush=True)
     paged.finish()
     print(f"  pager counts {paged.pager_counts()}", flush=True)
+
+
+@pytest.mark.parametrize("chunks", [1, 2])
+def test_host_banks_with_batched_calls(cuda, chunks):
+    """CFG-batched calls (batch 2, so banks = 2 x heads, as CogVideoX runs its two guidance
+    branches in one call, recap/models/cogvideox.py:109) with host banks, with and without
+    bank_chunks: paged == resident over REFRESH / SPARSE / REFRESH / SPARSE, validations
+    included."""
+    wl = SMALL["text-first-ragged"]
+    geometry = _geometry(wl)
+    layers = 2
+    resident, paged = _pair(wl, geometry, layers=layers, chunks=chunks)
+    q, k, v = make_qkv(wl, seed=7, batch=2, device=cuda)
+    schedule = [REFRESH, SPARSE, REFRESH, SPARSE]
+    for step, kind in enumerate(schedule):
+        inputs = tuple(perturb(x, 0.03, seed=j, step=step) for j, x in enumerate((q, k, v)))
+        stats = _run_step((resident, paged), step, kind,
+                          [(0, layer, inputs) for layer in range(layers)])
+        if stats is not None:
+            assert stats[0] == stats[1], (step, stats)
+        print(f"  step {step} {kind}: paged == resident (batch 2, chunks {chunks})", flush=True)
+    paged.finish()
+    counts = paged.pager_counts()
+    print(f"  pager counts {counts}", flush=True)
+    assert counts["copied"] == 0
