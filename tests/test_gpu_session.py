@@ -236,3 +236,51 @@ def test_session_with_the_gpu_operator_matches_the_session_with_the_oracle(cuda)
     assert {EXACT, REFRESH, SPARSE, REUSE} <= set(actions) and checked[SPARSE] > 0
     # the gains are fits to differences of bf16 outputs, each side rounded its own way
     assert max(abs(a - b) for a, b in gains) <= 2e-3, gains
+
+
+def test_two_stream_session_with_host_banks_equals_resident(cuda):
+    """Two transformer calls per step (two guidance branches, as Wan runs them,
+    recap/models/wan.py:22) through the step loop, once with resident banks and once with
+    host banks: the same actions, and every output equal bit for bit."""
+    from recap_amd import HostBankOperator
+
+    wl = SMALL["video-ragged-d128"]
+    steps = 12
+    base = [make_qkv(wl, seed=30 + s, device=cuda) for s in range(2)]
+    inputs = [[tuple(perturb(x, 0.02 * t, seed=10 * s + i, step=1) for i, x in enumerate(base[s]))
+               for s in range(2)] for t in range(steps)]
+    cfg = dataclasses.replace(
+        RecapConfig(), sync_step_timing=False,
+        geometry=GeometryConfig(grid=wl.grid, text_tokens=wl.text_tokens),
+        schedule=ScheduleConfig(num_steps=steps, tau=0.5, detail_tau_mult=1.0))
+    layout = Layout.from_permutation(hilbert_permutation(wl.grid), text_tokens=wl.text_tokens,
+                                     text_first=wl.text_first)
+    geo = SparseGeometry.build(layout, 128)
+
+    class TwoCalls:
+        def __init__(self, op):
+            self.op, self.calls = op, 0
+
+        def forward(self, t):
+            q, k, v = inputs[t][self.calls % 2]
+            self.calls += 1
+            return (torch.stack([self.op.attend(layer, q, k, v).float()
+                                 for layer in range(LAYERS)]),)
+
+    runs = []
+    for cls, host in ((Operator, False), (HostBankOperator, True)):
+        op = cls.build(OperatorConfig(head_density=wl.density, host_banks=host), geo,
+                       n_layers=LAYERS, n_streams=2)
+        tr = TwoCalls(op)
+        session = RecapSession(cfg, op, calls_per_step=2)
+        session.install(tr)
+        outs = [tr.forward(t)[0] for t in range(steps) for _ in range(2)]
+        if host:
+            op.finish()
+            print(f"  pager counts {op.pager_counts()}", flush=True)
+        runs.append(([r["a"] for r in session.actions], outs))
+    print(f"  schedule {runs[0][0]}", flush=True)
+    assert runs[0][0] == runs[1][0]
+    assert {REFRESH, SPARSE} <= set(runs[0][0])
+    for i, (a, b) in enumerate(zip(runs[0][1], runs[1][1])):
+        assert torch.equal(a, b), i
