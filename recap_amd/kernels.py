@@ -91,6 +91,12 @@ def prepare(x: torch.Tensor, name: str) -> torch.Tensor:
     return x
 
 
+def _same_type(q: torch.Tensor, kv: "PackedKV") -> None:
+    """The kernels read Q and the packed K/V tiles in one element type."""
+    if q.dtype != kv.dtype:
+        raise ValueError(f"Q is {q.dtype} but the packed K/V tiles are {kv.dtype}")
+
+
 def _qkv_args(x: torch.Tensor):
     b, h, _, d = x.shape
     return [x.data_ptr(), dtype_code(x.dtype), b, h, d, x.stride(0), x.stride(1), x.stride(2)]
@@ -306,6 +312,9 @@ def coarse_tail(q: torch.Tensor, rowmap: torch.Tensor, partition: torch.Tensor, 
                 tables: dict, scale: float, theta: float, glref: torch.Tensor | None = None):
     """(go [banks, R, d], gl [banks, R], drift partial [banks, R/128] or None).  `tables`
     holds the coarse tables and the closure rank they were built with (key "rank")."""
+    for key in ("kbar", "vbar", "w", "u_t", "cvk_t"):
+        if tables[key].dtype != q.dtype:
+            raise ValueError(f"coarse_tail: table {key} is {tables[key].dtype}, Q is {q.dtype}")
     b, h, n, d = q.shape
     banks = b * h
     partition = partition.contiguous()
@@ -336,6 +345,7 @@ def drift_center(part: torch.Tensor, geo: Geometry) -> torch.Tensor:
 def block_sparse_attn(q: torch.Tensor, kv: PackedKV, rowmap: torch.Tensor,
                       kernel_mask: torch.Tensor, geo: Geometry, scale: float):
     """Head branch (reordered order): (out [banks, N, d] in the query dtype, lse [banks, N])."""
+    _same_type(q, kv)
     b, h, n, d = q.shape
     kernel_mask = kernel_mask.contiguous()
     out = torch.empty(b * h, n, d, dtype=q.dtype, device=q.device)
@@ -349,6 +359,7 @@ def block_sparse_attn(q: torch.Tensor, kv: PackedKV, rowmap: torch.Tensor,
 def dense_attn(q: torch.Tensor, kv: PackedKV, rowmap: torch.Tensor, scale: float,
                out: torch.Tensor | None = None):
     """Dense attention, native order: (out [B, H, N, d], lse [B, H, N])."""
+    _same_type(q, kv)
     b, h, n, d = q.shape
     if out is None:
         out = torch.empty(b, h, n, d, dtype=q.dtype, device=q.device)
@@ -374,6 +385,7 @@ def dense_head_attn(q: torch.Tensor, kv: PackedKV, rowmap: torch.Tensor,
     (out [B, H, N, d] native, lse [B, H, N], head_out [banks, N, d] reordered in the query
     dtype, head_lse [banks, N]).  `balance` lets XCDs that finish early take the others' last query
     blocks (same outputs)."""
+    _same_type(q, kv)
     b, h, n, d = q.shape
     kernel_mask = kernel_mask.contiguous()
     if out is None:
@@ -394,6 +406,7 @@ def sparse_merge_attn(q: torch.Tensor, kv: PackedKV, rowmap: torch.Tensor,
                       out: torch.Tensor | None = None, balance: bool = True) -> torch.Tensor:
     """Corrected sparse output [B, H, N, d] in native order (one fused kernel); `balance` as
     for dense_head_attn."""
+    _same_type(q, kv)
     b, h, n, d = q.shape
     kernel_mask = kernel_mask.contiguous()
     if any(t is not None and not t.is_contiguous() for t in (go, gl, det, dl, glref, center)):

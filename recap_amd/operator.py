@@ -287,6 +287,8 @@ class Operator:
                                                   is_causal=False)
         if query.shape != key.shape or key.shape != value.shape:
             raise ValueError("Q/K/V shapes differ")
+        if not query.dtype == key.dtype == value.dtype:
+            raise ValueError(f"Q/K/V dtypes differ ({query.dtype}, {key.dtype}, {value.dtype})")
         chunks = int(self.config.bank_chunks)
         if chunks > 1:
             return self._attend_in_chunks(layer_index, query, key, value, chunks)

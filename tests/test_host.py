@@ -346,3 +346,26 @@ def test_no_refined_rows_needs_no_row_buffers():
     assert lib.recap_drift_center(None, 2, 100, 16, None) == _lib.RECAP_OK
     with pytest.raises(ValueError, match="NULL"):
         _lib.call("recap_drift_center", None, 2, 300, 16, None)
+
+
+def test_operator_rejects_mixed_qkv_dtypes():
+    """Q, K and V of different element types raise ValueError before any launch (the
+    kernels read them in one type; the reference's kernels and SDPA refuse them too); the
+    kernel wrappers check Q against the packed K/V tiles and the coarse tables."""
+    from recap_amd import REFRESH, Operator, OperatorConfig
+
+    layout = Layout.from_permutation(hilbert_permutation((1, 4, 32)), text_tokens=0,
+                                     text_first=False)
+    op = Operator.build(OperatorConfig(head_density=0.25), SparseGeometry.build(layout, 128),
+                        n_layers=1)
+    op.begin_step(0, REFRESH)
+    q = torch.zeros(1, 2, 128, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="dtypes differ"):
+        op.attend(0, q, q.to(torch.float16), q.to(torch.float16))
+    kv = K.PackedKV(*(torch.empty(0, dtype=torch.float16) for _ in range(2)),
+                    *(torch.empty(0) for _ in range(2)), torch.float16, 64)
+    with pytest.raises(ValueError, match="packed K/V tiles"):
+        K.block_sparse_attn(q, kv, None, torch.empty(0, dtype=torch.bool), None, 0.125)
+    tables = {n: torch.empty(0, dtype=torch.float16) for n in ("kbar", "vbar", "w", "u_t", "cvk_t")}
+    with pytest.raises(ValueError, match="table kbar"):
+        K.coarse_tail(q, None, torch.empty(0), None, tables, 0.125, 2.0)
